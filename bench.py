@@ -1,0 +1,337 @@
+"""Benchmark of the MI355X FlashAttention hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-configs]
+
+Prints ONE JSON line on stdout (everything else goes to stderr):
+
+* ``value``: causal prefill throughput in TFLOP/s at BASELINE config 3
+  (B=1, H=14, S=4096, D=64, fp16 in / fp32 accumulate), K timed steps, one
+  ``flashattn_cuda.prefill`` call per step, inputs resident in HBM, FLOPs by
+  the reference convention 4*B*H*S^2*D/2 (bench/run_bench.py:102-107).
+* ``roofline``: that kernel's achieved TFLOP/s from HIP events around each
+  launch in the timed region, against the dense fp16 MFMA peak.
+* ``decode``: BASELINE config 5 (ragged B=32, H=14, Lmax=4096) in GB/s of
+  algorithmic bytes (valid K/V rows + q + o + seq_lens) against 8 TB/s, with
+  the caches rotated over copies larger than the 256 MB MALL.
+* ``configs``: every BASELINE config with the reference's timing protocol
+  (10 warm-ups, 3 x 30 launches, median; bench/run_bench.py:83-99).
+* ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's
+  src/attention_cpu.py) timed on this host on a bounded sample of config 3.
+
+The CPU oracle is imported only for that baseline leg.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "flash-attention-cuda_amd"))
+sys.path.insert(0, REPO)
+
+MFMA_FP16_PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA (datasheet, no sparsity)
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+SCALE = 0.125
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def attention_flops(batch, heads, seq, causal, d=64):
+    f = 4.0 * batch * heads * seq * seq * d
+    return f * 0.5 if causal else f
+
+
+def decode_bytes(heads, lens, max_seq, d=64):
+    import torch
+
+    lens = torch.clamp(lens.long(), 0, max_seq)
+    b = lens.numel()
+    return 2 * heads * d * 2 * int(lens.sum()) + 2 * b * heads * d * 2 + 4 * b
+
+
+def cpu_inputs_prefill(batch, heads, seq, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq, 64)
+    return [torch.randn(shape, generator=g, dtype=torch.float32).half() for _ in range(3)]
+
+
+def cpu_inputs_decode(batch, heads, lmax, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, lmax + 1, (batch,), generator=g).to(torch.int32)
+    q = torch.randn((batch, heads, 1, 64), generator=g, dtype=torch.float32).half()
+    k = torch.randn((batch, heads, lmax, 64), generator=g, dtype=torch.float32).half()
+    v = torch.randn((batch, heads, lmax, 64), generator=g, dtype=torch.float32).half()
+    return q, k, v, lens
+
+
+def copies_for(nbytes, minimum=1):
+    """Number of input copies whose total exceeds 2x the MALL."""
+    return max(minimum, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
+
+
+def ref_timeit(fn_list, iters=30, warmup=10):
+    """bench/run_bench.py:83-99: median of three means over `iters` launches
+    (launch i uses fn_list[i % len(fn_list)] to rotate input copies)."""
+    import torch
+
+    n = len(fn_list)
+    for i in range(warmup):
+        fn_list[i % n]()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(3):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(iters):
+            fn_list[i % n]()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(end) / iters)
+    return sorted(samples)[1]
+
+
+def timed_steps(fn_list, steps, warmup):
+    """Contract timing: W untimed steps, then exactly K steps between
+    synchronisations; HIP events around every launch on the launch stream
+    give the kernel's average duration."""
+    import torch
+
+    n = len(fn_list)
+    for i in range(warmup):
+        fn_list[i % n]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record(stream)
+        fn_list[i % n]()
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    kern_ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
+    return wall_ms / steps, kern_ms
+
+
+def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup=0):
+    import torch
+
+    q, k, v = (t.cuda() for t in cpu_inputs_prefill(batch, heads, seq))
+    n = copies_for(3 * q.numel() * 2) if protocol == "ref" else 1
+    sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
+    fns = [lambda s=s: fa.prefill(s[0], s[1], s[2], causal, SCALE) for s in sets]
+    torch.cuda.synchronize()
+    flops = attention_flops(batch, heads, seq, causal)
+    if protocol == "ref":
+        ms = ref_timeit(fns)
+        return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "copies": n}
+    step_ms, kern_ms = timed_steps(fns, steps, warmup)
+    return {"ms_per_step": step_ms, "kernel_ms": kern_ms, "flops": flops}
+
+
+def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, warmup=0):
+    import torch
+
+    q, k, v, rl = cpu_inputs_decode(batch, heads, lmax)
+    if lens is not None:
+        rl = torch.tensor(lens, dtype=torch.int32)
+    q, k, v, rl = q.cuda(), k.cuda(), v.cuda(), rl.cuda()
+    n = copies_for(2 * k.numel() * 2)
+    sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
+    fns = [lambda s=s: fa.decode(s[0], s[1], s[2], rl, SCALE) for s in sets]
+    torch.cuda.synchronize()
+    nbytes = decode_bytes(heads, rl.cpu(), lmax)
+    if protocol == "ref":
+        ms = ref_timeit(fns)
+        return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "copies": n}
+    step_ms, kern_ms = timed_steps(fns, steps, warmup)
+    return {"ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": nbytes, "copies": n,
+            "sum_len": int(rl.sum().item())}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The CPU oracle on a bounded sample of config 3: causal heads of
+    B=1, S=4096 one at a time (one warm-up head, then heads until the budget
+    is spent), in TFLOP/s by the same causal FLOP convention."""
+    import numpy as np
+
+    from oracle import attention as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        blas_threads = 1
+    q, k, v = (t.numpy().astype(np.float32) for t in cpu_inputs_prefill(1, 14, 4096))
+    orc.attention_cpu(q[0, 0], k[0, 0], v[0, 0], SCALE, True)  # warm-up
+    t0 = time.perf_counter()
+    done = 0
+    while done < 14:
+        orc.attention_cpu(q[0, done], k[0, done], v[0, done], SCALE, True)
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    flops = attention_flops(1, done, 4096, True)
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(blas_threads),
+        "host_cpus": len(os.sched_getaffinity(0)),
+        "kind": "port",
+        "sample": f"config 3 (causal S=4096, D=64), {done} of 14 heads, fp32 numpy "
+                  f"restatement of src/attention_cpu.py with a causal mask, "
+                  f"{dt:.2f} s after one warm-up head",
+        "seconds_per_head": dt / done,
+    }
+
+
+def load_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(REPO, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config sweep")
+    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py measures one GPU only: this build has no multi-GPU path "
+            "(prefill and decode shard over (batch, head) with no exchange; see DESIGN.md). "
+            f"Requested --gpus {args.gpus}.")
+        sys.exit(2)
+
+    import torch
+
+    import flashattn_cuda as fa
+
+    if not torch.cuda.is_available():
+        log("no HIP device visible")
+        sys.exit(1)
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} ({props.multi_processor_count} CUs), "
+        f"arch {getattr(props, 'gcnArchName', '?')}")
+
+    result = {
+        "metric": "prefill TFLOP/s & %MFMA peak @S=4096; decode KV GB/s & %HBM peak",
+        "value": None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "config 3: causal prefill B=1 H=14 S=4096 D=64 "
+                               "(fp16 in, fp32 accumulate, fp16 out)",
+                   "batch": 1, "heads": 14, "seq_len": 4096, "head_dim": 64,
+                   "causal": True, "parallelism": "single GPU"},
+    }
+
+    if args.only in ("all", "prefill"):
+        log("timing config 3 prefill ...")
+        r = bench_prefill(fa, 1, 14, 4096, True, protocol="contract",
+                          steps=args.steps, warmup=args.warmup)
+        value = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
+        achieved = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+        result["value"] = value
+        result["ms_per_step"] = r["ms_per_step"]
+        result["roofline"] = {
+            "bound": "mfma",
+            "kernel": "prefill_kernel<causal=true>",
+            "achieved": achieved,
+            "peak": MFMA_FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
+            "kernel_ms": r["kernel_ms"],
+            "traffic": load_traffic("prefill_c3_traffic.txt"),
+        }
+        log(f"  {value:.1f} TFLOP/s per step, kernel {achieved:.1f} TFLOP/s "
+            f"({100 * achieved / MFMA_FP16_PEAK_TFLOPS:.1f}% of MFMA peak)")
+
+    if args.only in ("all", "decode"):
+        log("timing config 5 ragged decode ...")
+        d = bench_decode(fa, 32, 14, 4096, protocol="contract", steps=args.steps,
+                         warmup=args.warmup)
+        gbs_step = d["bytes"] / (d["ms_per_step"] * 1e-3) / 1e9
+        gbs_kern = d["bytes"] / (d["kernel_ms"] * 1e-3) / 1e9
+        result["decode"] = {
+            "workload": "config 5: ragged decode B=32 H=14 Lmax=4096 D=64, lens U[1,4096] seed 0",
+            "value": gbs_step,
+            "unit": "GB/s",
+            "ms_per_step": d["ms_per_step"],
+            "sum_len": d["sum_len"],
+            "bytes_per_step": d["bytes"],
+            "cache_copies_rotated": d["copies"],
+            "roofline": {"bound": "hbm", "kernel": "decode_split_kernel + decode_merge_kernel",
+                         "achieved": gbs_kern, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs_kern / HBM_PEAK_GBS, "kernel_ms": d["kernel_ms"],
+                         "traffic": load_traffic("decode_c5_traffic.txt")},
+        }
+        if args.only == "decode":
+            result["value"], result["unit"] = gbs_step, "GB/s"
+            result["ms_per_step"] = d["ms_per_step"]
+        log(f"  {gbs_step:.1f} GB/s per step ({100 * gbs_kern / HBM_PEAK_GBS:.1f}% of HBM peak)")
+
+    if not args.no_configs and args.only == "all":
+        log("reference-protocol sweep over the BASELINE configs ...")
+        rows = []
+        for name, b, h, s, c in [("C1 causal B1 H12 S128", 1, 12, 128, True),
+                                 ("C2 causal B4 H12 S1024", 4, 12, 1024, True),
+                                 ("C2 full B4 H12 S1024", 4, 12, 1024, False),
+                                 ("C3 causal B1 H14 S4096", 1, 14, 4096, True)]:
+            r = bench_prefill(fa, b, h, s, c)
+            rows.append({"config": name, "ms": r["ms"], "tflops": r["tflops"],
+                         "frac_mfma": r["tflops"] / MFMA_FP16_PEAK_TFLOPS})
+            log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['tflops']:.1f} TFLOP/s")
+        for name, b, h, lmax, lens in [("C4 decode B1 H12 L4096", 1, 12, 4096, [4096]),
+                                       ("C5 ragged decode B32 H14 Lmax4096", 32, 14, 4096, None)]:
+            r = bench_decode(fa, b, h, lmax, lens=lens)
+            rows.append({"config": name, "ms": r["ms"], "gbs": r["gbs"],
+                         "frac_hbm": r["gbs"] / HBM_PEAK_GBS, "copies": r["copies"]})
+            log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['gbs']:.1f} GB/s")
+        result["configs"] = rows
+
+    if not args.no_cpu:
+        log("CPU baseline (oracle, bounded sample) ...")
+        cb = cpu_baseline()
+        result["cpu_baseline"] = cb
+        log(f"  {cb['value'] * 1e3:.2f} GFLOP/s on {cb['cores']} threads")
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

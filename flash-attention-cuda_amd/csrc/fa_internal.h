@@ -1,0 +1,77 @@
+// Internal declarations shared by the gfx950 HIP sources of libflashattn_hip.
+//
+// Everything here is CDNA4-specific: wave64, 32x32x16 fp16 MFMA fragments,
+// DPP lane exchanges. Nothing is shared with, or adapted from, a CUDA path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "flashattn_hip.h"
+
+namespace fa {
+
+constexpr int kHeadDim = FA_HEAD_DIM;
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// MFMA fragment types for v_mfma_f32_32x32x16_f16: 8 halves in (A or B),
+// 16 fp32 accumulators out (a 32x32 tile over the 64 lanes).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---- host-side status plumbing (runtime.hip) -------------------------------
+// Record `msg` as the calling thread's last error and return `code`.
+int set_error(int code, const char *fmt, ...);
+void clear_error();
+// Check a HIP runtime result; on failure record it and return FA_ERR_HIP.
+int check_hip(hipError_t err, const char *what);
+// Compute-unit count of `device`, cached per device (0 on failure).
+int device_cu_count(int device);
+
+// ---- kernel launchers (prefill.hip / decode.hip) ---------------------------
+int launch_prefill(const void *q, const void *k, const void *v, void *o,
+                   bool out_f32, int batch, int heads, int seq, bool causal,
+                   float scale, hipStream_t stream);
+int launch_decode(const void *q, const void *k_cache, const void *v_cache,
+                  const int32_t *seq_lens, void *o, bool out_f32, int batch,
+                  int heads, int max_seq, float scale, int split_size,
+                  float *workspace, hipStream_t stream);
+
+// Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
+int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);
+int decode_occupancy(fa_occupancy_entry *out, int cap, int *n);
+int fill_occupancy_row(fa_occupancy_entry *row, const char *name,
+                       const void *func, int threads, int dyn_smem);
+
+// ---- device helpers --------------------------------------------------------
+// DPP lane permutations (gfx9 dpp_ctrl encodings). `bound_ctrl` is set so an
+// invalid source lane reads 0; every pattern used here stays inside its row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                         0xF, 0xF, true));
+}
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i inside 8 lanes
+
+// Sum over each aligned group of 8 lanes; every lane gets the group total.
+__device__ __forceinline__ float sum_lanes8(float x) {
+  x += dpp<kDppQuadXor1>(x);
+  x += dpp<kDppQuadXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+}  // namespace fa

@@ -1,0 +1,251 @@
+// C ABI of libflashattn_hip: argument checks, status codes, the split-K chunk
+// chooser, device queries and the occupancy report. The kernels themselves
+// live in prefill.hip and decode.hip.
+//
+// Argument checks mirror the pointer-level part of the reference's
+// validation (csrc/bindings.cpp:12-22, :39-64; csrc/decode.cu:209-211). The
+// tensor-level checks (device, dtype, contiguity, rank) belong to whoever
+// holds tensors: the pybind11 layer in bindings.cpp for Python callers.
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "fa_internal.h"
+
+namespace fa {
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_cu_once[kMaxDevices];
+int g_cu_count[kMaxDevices];
+
+bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+int check_hip(hipError_t err, const char *what) {
+  if (err == hipSuccess) return FA_OK;
+  return set_error(FA_ERR_HIP, "%s failed: %s (%s)", what,
+                   hipGetErrorString(err), hipGetErrorName(err));
+}
+
+int device_cu_count(int device) {
+  if (device < 0 || device >= kMaxDevices) return 0;
+  std::call_once(g_cu_once[device], [device] {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount,
+                              device) != hipSuccess)
+      cu = 0;
+    g_cu_count[device] = cu;
+  });
+  return g_cu_count[device];
+}
+
+int fill_occupancy_row(fa_occupancy_entry *row, const char *name,
+                       const void *func, int threads, int dyn_smem) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != FA_OK) return rc;
+  hipFuncAttributes attr{};
+  rc = check_hip(hipFuncGetAttributes(&attr, func), "hipFuncGetAttributes");
+  if (rc != FA_OK) return rc;
+  int blocks = 0;
+  rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, func,
+                                                              threads, dyn_smem),
+                 "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (rc != FA_OK) return rc;
+  int max_threads = 0;
+  rc = check_hip(hipDeviceGetAttribute(
+                     &max_threads,
+                     hipDeviceAttributeMaxThreadsPerMultiProcessor, dev),
+                 "hipDeviceGetAttribute");
+  if (rc != FA_OK) return rc;
+  std::memset(row, 0, sizeof(*row));
+  std::snprintf(row->kernel, sizeof(row->kernel), "%s", name);
+  row->threads_per_block = threads;
+  row->registers_per_thread = attr.numRegs;
+  row->shared_bytes_per_block = static_cast<int>(attr.sharedSizeBytes) + dyn_smem;
+  row->max_active_blocks_per_sm = blocks;
+  row->theoretical_occupancy =
+      max_threads > 0 ? static_cast<double>(blocks) * threads / max_threads : 0.0;
+  return FA_OK;
+}
+
+}  // namespace fa
+
+using namespace fa;
+
+extern "C" {
+
+const char *fa_version(void) { return "2.0.0-gfx950"; }
+
+int fa_head_dim(void) { return FA_HEAD_DIM; }
+
+const char *fa_last_error(void) { return g_last_error; }
+
+// csrc/decode.cu:183-192: the largest power-of-two chunk in [128, 1024] that
+// still yields min_blocks split blocks; otherwise the smallest chunk.
+int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks) {
+  const int64_t per_split = static_cast<int64_t>(batch) * heads;
+  for (int split = FA_DECODE_SPLIT_MAX; split > FA_DECODE_SPLIT_MIN;
+       split >>= 1) {
+    const int64_t splits = (static_cast<int64_t>(max_seq) + split - 1) / split;
+    if (per_split * splits >= min_blocks) return split;
+  }
+  return FA_DECODE_SPLIT_MIN;
+}
+
+// csrc/decode.cu:205-206: two blocks per compute unit.
+int fa_decode_min_blocks(int device, int *min_blocks) {
+  clear_error();
+  if (min_blocks == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "min_blocks must not be NULL");
+  const int cu = device_cu_count(device);
+  if (cu <= 0)
+    return set_error(FA_ERR_HIP, "could not query the compute-unit count of device %d",
+                     device);
+  *min_blocks = 2 * cu;
+  return FA_OK;
+}
+
+size_t fa_prefill_workspace_bytes(int, int, int, int) { return 0; }
+
+int fa_prefill(const void *q, const void *k, const void *v, void *o,
+               int out_dtype, int batch, int heads, int seq, int causal,
+               float scale, void *workspace, size_t workspace_bytes,
+               void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  clear_error();
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "q, k, v and o must be 16-byte aligned device pointers");
+  if (out_dtype != FA_OUT_F16 && out_dtype != FA_OUT_F32)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "unknown out_dtype %d", out_dtype);
+  if (batch <= 0 || heads <= 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "batch and heads must be > 0, got B=%d H=%d", batch, heads);
+  if (seq <= 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "sequence length must be > 0");
+  if (static_cast<int64_t>(batch) * heads * ((static_cast<int64_t>(seq) + 127) / 128) >
+      0x7fffffffll)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "batch * heads * seq too large");
+  if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
+    return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  return launch_prefill(q, k, v, o, out_dtype == FA_OUT_F32, batch, heads, seq,
+                        causal != 0, scale, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+// Resolves split_size 0 to the automatic choice; returns an fa_status.
+int resolve_split(int batch, int heads, int max_seq, int *split_size) {
+  if (*split_size < 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "decode split size must be >= 0, got %d", *split_size);
+  if (*split_size == 0) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != FA_OK) return rc;
+    int min_blocks = 0;
+    rc = fa_decode_min_blocks(dev, &min_blocks);
+    if (rc != FA_OK) return rc;
+    *split_size = fa_choose_decode_split(max_seq, batch, heads, min_blocks);
+  }
+  // csrc/decode.cu:209-211.
+  if (*split_size % 4 != 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "decode split size must be a multiple of the warp count, got %d",
+                     *split_size);
+  return FA_OK;
+}
+
+size_t decode_ws_bytes(int batch, int heads, int max_seq, int split) {
+  const size_t n_splits = (static_cast<size_t>(max_seq) + split - 1) / split;
+  return static_cast<size_t>(batch) * heads * n_splits * (FA_HEAD_DIM + 2) *
+         sizeof(float);
+}
+}  // namespace
+
+size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
+                                 int split_size) {
+  clear_error();
+  if (batch <= 0 || heads <= 0 || max_seq <= 0) {
+    set_error(FA_ERR_INVALID_ARGUMENT, "batch, heads and max_seq must be > 0");
+    return 0;
+  }
+  if (resolve_split(batch, heads, max_seq, &split_size) != FA_OK) return 0;
+  return decode_ws_bytes(batch, heads, max_seq, split_size);
+}
+
+int fa_decode(const void *q, const void *k_cache, const void *v_cache,
+              const int32_t *seq_lens, void *o, int out_dtype, int batch,
+              int heads, int max_seq, float scale, int split_size,
+              void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
+      seq_lens == nullptr || o == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "q, k_cache, v_cache, seq_lens and o must be non-NULL");
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) ||
+      !aligned16(o))
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "q, k_cache, v_cache and o must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "seq_lens must be 4-byte aligned");
+  if (out_dtype != FA_OUT_F16 && out_dtype != FA_OUT_F32)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "unknown out_dtype %d", out_dtype);
+  if (batch <= 0 || heads <= 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "batch and heads must be > 0, got B=%d H=%d", batch, heads);
+  if (max_seq <= 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be > 0");
+  if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
+    return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  int rc = resolve_split(batch, heads, max_seq, &split_size);
+  if (rc != FA_OK) return rc;
+  const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
+  if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "too many split blocks");
+  const size_t need = decode_ws_bytes(batch, heads, max_seq, split_size);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(FA_ERR_WORKSPACE,
+                     "decode workspace too small: need %zu bytes, got %zu", need,
+                     workspace == nullptr ? size_t{0} : workspace_bytes);
+  if (!aligned16(workspace))
+    return set_error(FA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  return launch_decode(q, k_cache, v_cache, seq_lens, o, out_dtype == FA_OUT_F32,
+                       batch, heads, max_seq, scale, split_size,
+                       static_cast<float *>(workspace),
+                       static_cast<hipStream_t>(stream));
+}
+
+int fa_occupancy_report(fa_occupancy_entry *out, int capacity, int *count) {
+  clear_error();
+  if (count == nullptr || (capacity > 0 && out == nullptr))
+    return set_error(FA_ERR_INVALID_ARGUMENT, "bad occupancy report buffer");
+  int n = 0;
+  int rc = prefill_occupancy(out, capacity, &n);
+  if (rc == FA_OK) rc = decode_occupancy(out, capacity, &n);
+  *count = n;
+  return rc;
+}
+
+}  // extern "C"

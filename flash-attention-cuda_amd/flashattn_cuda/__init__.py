@@ -1,0 +1,58 @@
+"""Batched multi-head causal FlashAttention kernels for head_dim = 64, on MI355X.
+
+Drop-in for the reference package's API (flashattn_cuda/__init__.py:1-31 of
+shrvan30/flash-attention-cuda): ``prefill``, ``decode``, ``head_dim``,
+``occupancy_report``, ``choose_decode_split`` and the ``_decode_with_split``
+benchmark hook, with the same tensor layouts ([B, H, N, 64] fp16 on the
+``cuda`` device, which is the HIP device on ROCm) and the same errors.
+
+The v1 ``legacy_naive/tiled/fused`` teaching kernels of the reference are
+not part of this build; touching them raises ``NotImplementedError``.
+
+There is no fallback: if the compiled extension ``_C`` (and the HIP library
+``libflashattn_hip.so`` it links) is missing, importing this package fails.
+"""
+
+# The extension links libc10/libtorch, which are only on the loader's path
+# once torch itself has been imported (same reason as the reference).
+import torch as _torch  # noqa: F401
+
+try:
+    from ._C import (  # noqa: F401
+        _decode_fp32,
+        _decode_with_split,
+        _prefill_fp32,
+        choose_decode_split,
+        decode,
+        head_dim,
+        occupancy_report,
+        prefill,
+    )
+except ImportError as exc:  # pragma: no cover - exercised only when unbuilt
+    raise ImportError(
+        "flashattn_cuda: the gfx950 extension is not built. Run "
+        "`python flash-attention-cuda_amd/build.py` (or __graft_entry__.build()) "
+        f"first. Underlying error: {exc}"
+    ) from exc
+
+
+def _legacy_unavailable(*_args, **_kwargs):
+    raise NotImplementedError(
+        "the v1 legacy_* fp32 teaching kernels are not part of the MI355X build"
+    )
+
+
+legacy_naive = legacy_tiled = legacy_fused = _legacy_unavailable
+
+__all__ = [
+    "prefill",
+    "decode",
+    "head_dim",
+    "occupancy_report",
+    "choose_decode_split",
+    "legacy_naive",
+    "legacy_tiled",
+    "legacy_fused",
+]
+
+__version__ = "2.0.0"

@@ -1,0 +1,124 @@
+/*
+ * flashattn_hip.h — C ABI of the MI355X (gfx950) FlashAttention library
+ * (libflashattn_hip.so).
+ *
+ * The ABI carries plain device pointers, sizes and a HIP stream handle. It
+ * has no torch types, so ctypes, cgo, JNI or a C++ host can bind it directly.
+ * The Python package `flashattn_cuda` wraps it with the reference's
+ * pybind11 surface (`prefill`, `decode`, `_decode_with_split`,
+ * `choose_decode_split`, `occupancy_report`, `head_dim`).
+ *
+ * Reference interface that each entry point replaces
+ * (paths relative to shrvan30/flash-attention-cuda):
+ *   fa_head_dim              <- kHeadDim          csrc/flash_common.h:11,
+ *                                                 bindings.cpp:112 (m.attr)
+ *   fa_choose_decode_split   <- choose_decode_split  csrc/decode.cu:183-192,
+ *                                                 bindings.cpp:122-125
+ *   fa_decode_min_blocks     <- min_blocks = 2 * multiProcessorCount
+ *                                                 csrc/decode.cu:205-206
+ *   fa_prefill_workspace_bytes, fa_prefill
+ *                            <- launch_prefill    csrc/prefill.cu:347-373
+ *                               (called by prefill, bindings.cpp:10-27)
+ *   fa_decode_workspace_bytes, fa_decode
+ *                            <- launch_decode     csrc/decode.cu:194-240
+ *                               (called by decode_impl, bindings.cpp:36-76)
+ *   fa_occupancy_report      <- prefill_occupancy / decode_occupancy
+ *                               csrc/prefill.cu:375-394, csrc/decode.cu:242-261
+ *
+ * Tensor layout (same as the reference): q, k, v, o are [B, H, S, 64]
+ * contiguous fp16 (IEEE binary16); a decode cache is [B, H, Lmax, 64]; the
+ * decode query and output are [B, H, 1, 64]; seq_lens is [B] int32 in device
+ * memory. Every pointer must be a device pointer aligned to 16 bytes.
+ *
+ * Launches are asynchronous on `stream` (a hipStream_t; NULL is the default
+ * stream) and never synchronise the host. A non-zero return value is an
+ * fa_status; fa_last_error() then returns a message for the calling thread.
+ */
+#ifndef FLASHATTN_HIP_H_
+#define FLASHATTN_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_HEAD_DIM 64
+#define FA_DECODE_SPLIT_MIN 128  /* csrc/flash_common.h:21 */
+#define FA_DECODE_SPLIT_MAX 1024 /* csrc/flash_common.h:22 */
+
+typedef enum fa_status {
+  FA_OK = 0,
+  FA_ERR_INVALID_ARGUMENT = 1, /* bad size, pointer, alignment or scale */
+  FA_ERR_WORKSPACE = 2,        /* workspace missing or too small */
+  FA_ERR_HIP = 3               /* a HIP runtime call or launch failed */
+} fa_status;
+
+/* Output element type. FA_OUT_F16 is the public contract; FA_OUT_F32 writes
+ * the same kernels' fp32 result before the final rounding (a parity hook). */
+typedef enum fa_out_dtype { FA_OUT_F16 = 0, FA_OUT_F32 = 1 } fa_out_dtype;
+
+/* One row of the occupancy report (bindings.cpp:80-97 dict keys). */
+typedef struct fa_occupancy_entry {
+  char kernel[64];
+  int threads_per_block;
+  int registers_per_thread;
+  int shared_bytes_per_block;
+  int max_active_blocks_per_sm;
+  double theoretical_occupancy;
+} fa_occupancy_entry;
+
+/* Library version string, e.g. "2.0.0-gfx950". */
+const char *fa_version(void);
+
+/* The head size every kernel is specialised for: 64. */
+int fa_head_dim(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char *fa_last_error(void);
+
+/* Largest power-of-two chunk C in [128, 1024] with
+ * batch * heads * ceil(max_seq / C) >= min_blocks, else 128. Pure integer
+ * function of its arguments. */
+int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks);
+
+/* Block target the automatic chunk choice uses on `device`:
+ * 2 * (compute units). Returns an fa_status. */
+int fa_decode_min_blocks(int device, int *min_blocks);
+
+/* Bytes of device workspace fa_prefill needs for this shape (may be 0). */
+size_t fa_prefill_workspace_bytes(int batch, int heads, int seq, int causal);
+
+/* o = softmax(q k^T * scale [+ causal mask]) v for every (b, h).
+ * causal: query row i attends keys 0..i. fp32 accumulation throughout.
+ * workspace may be NULL when fa_prefill_workspace_bytes(...) is 0. */
+int fa_prefill(const void *q, const void *k, const void *v, void *o,
+               int out_dtype, int batch, int heads, int seq, int causal,
+               float scale, void *workspace, size_t workspace_bytes,
+               void *stream);
+
+/* Bytes of device workspace fa_decode needs. split_size 0 selects the chunk
+ * the same way fa_decode does (it queries the current device). Returns 0 and
+ * sets fa_last_error() on invalid arguments. */
+size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
+                                 int split_size);
+
+/* Single-query attention against a KV cache: sequence b attends cache rows
+ * [0, min(seq_lens[b], max_seq)); a sequence with seq_lens[b] <= 0 gets a
+ * zero output. split_size 0 chooses the split-K chunk automatically; a
+ * positive value forces it and must be a multiple of 4. */
+int fa_decode(const void *q, const void *k_cache, const void *v_cache,
+              const int32_t *seq_lens, void *o, int out_dtype, int batch,
+              int heads, int max_seq, float scale, int split_size,
+              void *workspace, size_t workspace_bytes, void *stream);
+
+/* Fill up to `capacity` entries (one per kernel) for the current device;
+ * *count receives the number of kernels. Returns an fa_status. */
+int fa_occupancy_report(fa_occupancy_entry *out, int capacity, int *count);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FLASHATTN_HIP_H_ */

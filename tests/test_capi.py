@@ -1,0 +1,158 @@
+"""CPU-side checks of the C ABI (include/flashattn_hip.h, libflashattn_hip.so).
+
+No test here launches a kernel or touches a device: they cover symbol
+export, the pure integer entry points and the argument checks that fail
+before any HIP call.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER_DIR = os.path.join(REPO, "include")
+LIB = os.path.join(REPO, "flash-attention-cuda_amd", "flashattn_cuda", "libflashattn_hip.so")
+
+FA_OK, FA_ERR_INVALID_ARGUMENT, FA_ERR_WORKSPACE, FA_ERR_HIP = 0, 1, 2, 3
+
+
+def declared_functions():
+    names = []
+    for fn in sorted(os.listdir(HEADER_DIR)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(HEADER_DIR, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(fa_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built; run flash-attention-cuda_amd/build.py")
+    dll = ctypes.CDLL(LIB)
+    dll.fa_last_error.restype = ctypes.c_char_p
+    dll.fa_version.restype = ctypes.c_char_p
+    dll.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+    dll.fa_prefill_workspace_bytes.restype = ctypes.c_size_t
+    return dll
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted(
+        [
+            "fa_choose_decode_split",
+            "fa_decode",
+            "fa_decode_min_blocks",
+            "fa_decode_workspace_bytes",
+            "fa_head_dim",
+            "fa_last_error",
+            "fa_occupancy_report",
+            "fa_prefill",
+            "fa_prefill_workspace_bytes",
+            "fa_version",
+        ]
+    )
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing
+
+
+def test_head_dim_and_version(lib):
+    assert lib.fa_head_dim() == 64
+    assert lib.fa_version().decode().startswith("2.0.0")
+
+
+def test_choose_decode_split_matches_oracle(lib):
+    for max_seq in (1, 63, 128, 129, 512, 1000, 2048, 4096, 65536):
+        for batch, heads in ((1, 1), (1, 12), (2, 12), (8, 12), (32, 14)):
+            for target in (164, 512, 608, 4096):
+                assert lib.fa_choose_decode_split(max_seq, batch, heads, target) == \
+                    oracle.choose_decode_split(max_seq, batch, heads, target)
+
+
+def test_decode_workspace_bytes_forced_split(lib):
+    # [B, H, n_splits, 64] + [B, H, n_splits, 2] fp32 (decode.cu:215-219).
+    assert lib.fa_decode_workspace_bytes(32, 14, 4096, 1024) == 32 * 14 * 4 * 66 * 4
+    assert lib.fa_decode_workspace_bytes(1, 12, 4096, 128) == 12 * 32 * 66 * 4
+    assert lib.fa_decode_workspace_bytes(1, 12, 4096, 6) == 0  # not a multiple of 4
+    assert b"multiple of the warp count" in lib.fa_last_error()
+    assert lib.fa_decode_workspace_bytes(0, 12, 4096, 128) == 0
+
+
+def test_prefill_rejects_bad_arguments_before_any_launch(lib):
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    f = ctypes.c_float
+    rc = lib.fa_prefill(None, p, p, p, 0, 1, 1, 8, 1, f(0.125), None, ctypes.c_size_t(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"non-NULL" in lib.fa_last_error()
+    odd = ctypes.c_void_p(p.value + 2)
+    rc = lib.fa_prefill(odd, p, p, p, 0, 1, 1, 8, 1, f(0.125), None, ctypes.c_size_t(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"aligned" in lib.fa_last_error()
+    rc = lib.fa_prefill(p, p, p, p, 0, 1, 1, 0, 1, f(0.125), None, ctypes.c_size_t(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"sequence length must be > 0" in lib.fa_last_error()
+    rc = lib.fa_prefill(p, p, p, p, 0, 1, 1, 8, 1, f(float("inf")), None, ctypes.c_size_t(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"scale must be finite" in lib.fa_last_error()
+    rc = lib.fa_prefill(p, p, p, p, 7, 1, 1, 8, 1, f(0.125), None, ctypes.c_size_t(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"out_dtype" in lib.fa_last_error()
+
+
+def test_decode_rejects_bad_arguments_before_any_launch(lib):
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    f = ctypes.c_float
+    sz = ctypes.c_size_t
+    rc = lib.fa_decode(p, p, p, None, p, 0, 1, 2, 8, f(0.125), 128, p, sz(1 << 16), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"non-NULL" in lib.fa_last_error()
+    rc = lib.fa_decode(p, p, p, p, p, 0, 1, 2, 0, f(0.125), 128, p, sz(1 << 16), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"cache length must be > 0" in lib.fa_last_error()
+    rc = lib.fa_decode(p, p, p, p, p, 0, 1, 2, 8, f(0.125), 130, p, sz(1 << 16), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"multiple of the warp count" in lib.fa_last_error()
+    rc = lib.fa_decode(p, p, p, p, p, 0, 1, 2, 8, f(0.125), 128, p, sz(16), None)
+    assert rc == FA_ERR_WORKSPACE and b"workspace too small" in lib.fa_last_error()
+    rc = lib.fa_decode(p, p, p, p, p, 0, 1, 2, 8, f(float("nan")), 128, p, sz(1 << 16), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"scale must be finite" in lib.fa_last_error()
+
+
+def test_python_package_exposes_reference_surface():
+    """flashattn_cuda/__init__.py:20-29 of the reference (legacy_* stubbed)."""
+    import flashattn_cuda as fa
+
+    for name in ("prefill", "decode", "head_dim", "occupancy_report", "choose_decode_split",
+                 "_decode_with_split", "legacy_naive", "legacy_tiled", "legacy_fused"):
+        assert hasattr(fa, name), name
+    assert fa.head_dim == 64 and fa.__version__ == "2.0.0"
+    assert fa.choose_decode_split(512, 1, 12, 512) == 128
+    assert fa.choose_decode_split(max_seq=4096, batch=32, heads=14, min_blocks=512) == 1024
+    with pytest.raises(NotImplementedError):
+        fa.legacy_fused(None, None, None)
+
+
+def test_python_rejects_cpu_tensors_without_a_device():
+    """'must be a CUDA tensor' (tests/test_correctness.py:213-214) needs no GPU."""
+    import torch
+
+    import flashattn_cuda as fa
+
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        fa.prefill(q, q, q, True, 0.125)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        fa.decode(q[:, :, :1], q, q, torch.tensor([4], dtype=torch.int32), 0.125)
+    # The device check comes first (flash_common.h:55-57), so a CPU fp32
+    # tensor is reported as "not a CUDA tensor", as in the reference.
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        fa.prefill(q.float(), q.float(), q.float(), True, 0.125)
+
+
+def test_seq_lens_sum_of_baseline_instance():
+    lens = np.asarray(oracle.make_decode_inputs(32, 14, 8, seed=0)[3])
+    assert lens.shape == (32,)

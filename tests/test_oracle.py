@@ -1,0 +1,319 @@
+"""Pin the CPU oracle (oracle/attention.py) before it is trusted as a checker.
+
+Every oracle function is checked against something that does not share its
+code: the committed fp64 brute-force fixtures, an fp64 loop written here,
+torch's CPU scaled_dot_product_attention, closed forms and invariants. The
+last group plants plausible mistakes in copies of the oracle and requires the
+same checks to reject them, so the checks are known to have teeth.
+"""
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import attention as orc
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+D = 64
+SCALE = 0.125
+
+
+def _rand(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).half()
+
+
+def _fixtures():
+    return sorted(glob.glob(os.path.join(GOLDEN, "*.npz")))
+
+
+def _load(path):
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+# ---------------------------------------------------------------------------
+# Checks (reused by the planted-mistake tests below)
+# ---------------------------------------------------------------------------
+
+
+def check_prefill_fn(prefill_fn, tol=2e-6):
+    """Raise AssertionError if `prefill_fn` disagrees with the pins."""
+    for path in _fixtures():
+        c = _load(path)
+        if str(c["kind"]) != "prefill":
+            continue
+        got = prefill_fn(c["q"], c["k"], c["v"], bool(c["causal"]), float(c["scale"]))
+        err = np.abs(got.astype(np.float64) - c["out"]).max()
+        assert err <= tol, f"{os.path.basename(path)}: {err}"
+    # torch CPU SDPA, fp32, causal and full.
+    q, k, v = (_rand((2, 3, 75, D), s) for s in (1, 2, 3))
+    for causal in (True, False):
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float(), v.float(), is_causal=causal, scale=SCALE
+        ).numpy()
+        got = prefill_fn(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+        assert np.abs(got - ref).max() <= 1e-5
+
+
+def check_decode_fn(decode_fn, tol=2e-6):
+    for path in _fixtures():
+        c = _load(path)
+        if str(c["kind"]) != "decode":
+            continue
+        got = decode_fn(c["q"], c["k"], c["v"], c["lens"], float(c["scale"]))
+        err = np.abs(got.astype(np.float64) - c["out"]).max()
+        assert err <= tol, f"{os.path.basename(path)}: {err}"
+
+
+# ---------------------------------------------------------------------------
+# The oracle against the pins
+# ---------------------------------------------------------------------------
+
+
+def test_golden_fixtures_present():
+    names = {os.path.basename(p) for p in _fixtures()}
+    assert "prefill_causal_s130.npz" in names and "decode_edges.npz" in names
+    assert len(names) == 9
+
+
+def test_prefill_matches_pins():
+    check_prefill_fn(oracle.prefill)
+
+
+def test_decode_matches_pins():
+    check_decode_fn(oracle.decode)
+
+
+def test_attention_cpu_matches_fp64_loop():
+    """attention_cpu (fp32, vectorised) vs an fp64 loop written here."""
+    rng = np.random.default_rng(5)
+    Q = rng.standard_normal((6, D)).astype(np.float32)
+    K = rng.standard_normal((9, D)).astype(np.float32)
+    V = rng.standard_normal((9, D)).astype(np.float32)
+    for causal in (False, True):
+        got = oracle.attention_cpu(Q, K, V, SCALE, causal)
+        for i in range(6):
+            n = i + 1 + 3 if causal else 9  # bottom-right aligned: M - N = 3
+            s = [sum(float(Q[i, d]) * float(K[j, d]) for d in range(D)) * SCALE for j in range(n)]
+            m = max(s)
+            w = [math.exp(x - m) for x in s]
+            want = [sum(w[j] * float(V[j, d]) for j in range(n)) / sum(w) for d in range(D)]
+            assert np.abs(got[i] - np.array(want)).max() < 2e-6
+
+
+def test_default_scale_is_inverse_sqrt_d():
+    """attention_cpu.py:37-38: scale defaults to 1/sqrt(d)."""
+    rng = np.random.default_rng(6)
+    Q, K, V = (rng.standard_normal((5, D)).astype(np.float32) for _ in range(3))
+    np.testing.assert_allclose(oracle.attention_cpu(Q, K, V), oracle.attention_cpu(Q, K, V, 0.125), rtol=0, atol=0)
+
+
+def test_stable_softmax_rows_and_shift_invariance():
+    x = np.array([[1.0, 2.0, 3.0], [1000.0, 1001.0, -np.inf]], dtype=np.float32)
+    p = oracle.stable_softmax(x)
+    np.testing.assert_allclose(p.sum(-1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(p[0], oracle.stable_softmax(x[:1] + 50.0)[0], rtol=1e-6)
+    assert p[1, 2] == 0.0
+    e = np.exp([-2.0, -1.0, 0.0])
+    np.testing.assert_allclose(p[0], e / e.sum(), rtol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_constant_value_rows_give_that_row(causal):
+    q, k, _ = (_rand((1, 2, 40, D), s) for s in (7, 8, 9))
+    row = _rand((D,), 10)
+    v = row.expand(1, 2, 40, D).contiguous()
+    out = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    np.testing.assert_allclose(out, np.broadcast_to(row.float().numpy(), out.shape), atol=2e-6)
+
+
+def test_scale_zero_gives_visible_mean():
+    q, k, v = (_rand((1, 1, 33, D), s) for s in (11, 12, 13))
+    out = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), True, 0.0)
+    vf = v.float().numpy()[0, 0]
+    want = np.cumsum(vf, axis=0) / np.arange(1, 34)[:, None]
+    np.testing.assert_allclose(out[0, 0], want, atol=2e-6)
+    full = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), False, 0.0)
+    np.testing.assert_allclose(full[0, 0], np.broadcast_to(vf.mean(0), (33, D)), atol=2e-6)
+
+
+def test_causal_row0_is_v_row0():
+    q, k, v = (_rand((2, 2, 17, D), s) for s in (14, 15, 16))
+    out = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), True, SCALE)
+    np.testing.assert_array_equal(out[:, :, 0], v.float().numpy()[:, :, 0])
+
+
+def test_full_attention_is_key_permutation_invariant():
+    q, k, v = (_rand((1, 2, 50, D), s) for s in (17, 18, 19))
+    perm = torch.randperm(50, generator=torch.Generator().manual_seed(3))
+    a = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), False, SCALE)
+    b = oracle.prefill(q.numpy(), k[:, :, perm].numpy(), v[:, :, perm].numpy(), False, SCALE)
+    np.testing.assert_allclose(a, b, atol=2e-6)
+
+
+def test_decode_equals_causal_prefill_row():
+    """tests/test_correctness.py:94-110, on the oracle."""
+    q, k, v = (_rand((2, 3, 90, D), s) for s in (20, 21, 22))
+    full = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), True, SCALE)
+    for t in (0, 1, 17, 63, 64, 89):
+        lens = np.full((2,), t + 1, dtype=np.int32)
+        out = oracle.decode(q[:, :, t : t + 1].numpy(), k.numpy(), v.numpy(), lens, SCALE)
+        np.testing.assert_allclose(out[:, :, 0], full[:, :, t], atol=2e-6)
+
+
+def test_decode_clamps_and_zeroes():
+    """decode.cu:69 (len > Lmax clamps) and :155-172 (len <= 0 gives 0)."""
+    q = _rand((3, 2, 1, D), 23).numpy()
+    k, v = (_rand((3, 2, 12, D), s).numpy() for s in (24, 25))
+    out = oracle.decode(q, k, v, np.array([0, 50, -4], dtype=np.int32), SCALE)
+    ref = oracle.decode(q, k, v, np.array([0, 12, 0], dtype=np.int32), SCALE)
+    np.testing.assert_array_equal(out, ref)
+    assert not out[0].any() and not out[2].any()
+
+
+def test_decode_matches_torch_loop():
+    """The reference's own decode oracle form (tests/test_correctness.py:37-44)."""
+    q = _rand((3, 4, 1, D), 26)
+    k, v = (_rand((3, 4, 200, D), s) for s in (27, 28))
+    lens = torch.tensor([200, 1, 77], dtype=torch.int32)
+    want = torch.empty(3, 4, 1, D)
+    for b in range(3):
+        n = int(lens[b])
+        s = (q[b].float() @ k[b, :, :n].float().transpose(-1, -2).contiguous()) * SCALE
+        want[b] = torch.softmax(s, dim=-1) @ v[b, :, :n].float()
+    got = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    np.testing.assert_allclose(got, want.numpy(), atol=2e-6)
+
+
+# ---------------------------------------------------------------------------
+# Chooser, FLOP and byte formulas
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("sms", [82, 256, 304])
+def test_choose_decode_split_pins(sms):
+    """tests/test_correctness.py:180-198, restated so it holds for any CU
+    count: either the target is reached and doubling the chunk falls short,
+    or the chunk is the 128 fallback."""
+    target = 2 * sms
+    for batch, heads, seq in [(1, 12, 2048), (8, 12, 2048), (4, 12, 1024), (32, 14, 4096), (1, 12, 4096)]:
+        split = oracle.choose_decode_split(seq, batch, heads, target)
+        assert split in (128, 256, 512, 1024)
+        blocks = batch * heads * -(-seq // split)
+        if split > 128:
+            assert blocks >= target
+        if split < 1024 and blocks >= target:
+            assert batch * heads * -(-seq // (split * 2)) < target
+        if blocks < target:
+            assert split == 128
+    assert oracle.choose_decode_split(512, 1, 12, target) == 128
+
+
+def test_choose_decode_split_reference_asserts_hold_on_3090():
+    """On the reference's 82-SM card the original asserts hold verbatim."""
+    target = 2 * 82
+    for batch, heads, seq in [(1, 12, 2048), (8, 12, 2048), (4, 12, 1024)]:
+        split = oracle.choose_decode_split(seq, batch, heads, target)
+        assert batch * heads * -(-seq // split) >= target
+        if split < 1024:
+            assert batch * heads * -(-seq // (split * 2)) < target
+
+
+def test_choose_decode_split_baseline_configs():
+    # MI355X: 256 CUs -> min_blocks 512.
+    assert oracle.choose_decode_split(4096, 1, 12, 512) == 128   # C4: 384 blocks, fallback
+    assert oracle.choose_decode_split(4096, 32, 14, 512) == 1024  # C5: 1792 blocks
+    # analysis.md:113 on the 3090 (164 target): B1 H12 S4096 -> chunk 256.
+    assert oracle.choose_decode_split(4096, 1, 12, 164) == 256
+
+
+def test_flops_and_bytes():
+    assert oracle.attention_flops(1, 12, 128, True) == 25_165_824
+    assert oracle.attention_flops(1, 14, 4096, True) == 30_064_771_072
+    assert oracle.attention_flops(4, 12, 1024, False) == 12_884_901_888
+    assert oracle.decode_bytes(12, [4096], 4096) == 12_585_988
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(1, 4097, (32,), generator=g)
+    assert int(lens.sum()) == 73_374
+    assert oracle.decode_bytes(14, lens.numpy(), 4096) == 263_087_232
+
+
+def test_fp16_floor_helpers():
+    assert orc.fp16_half_ulp(np.array([0.75]))[0] == 2.0 ** -12
+    assert orc.fp16_half_ulp(np.array([3.0]))[0] == 2.0 ** -10
+    assert orc.fp16_rounding_floor(np.array([1.0, 0.5], dtype=np.float32)) == 0.0
+
+
+# ---------------------------------------------------------------------------
+# Planted mistakes: each mutant must fail the checks above.
+# ---------------------------------------------------------------------------
+
+
+def _mutant_prefill(kind):
+    def attn(Q, K, V, scale, causal):
+        N, d = Q.shape
+        S = (Q @ K.T) * np.float32(scale)
+        if kind == "scores_transposed":  # S^T where S was meant
+            S = (K @ Q.T) * np.float32(scale)
+        if kind == "scale_twice":
+            S = S * np.float32(scale)
+        if causal:
+            i = np.arange(N)[:, None]
+            j = np.arange(K.shape[0])[None, :]
+            keep = (j < i) | ((i == 0) & (j == 0)) if kind == "mask_edge" else j <= i
+            S = np.where(keep, S, np.float32(-np.inf))
+        P = orc.stable_softmax(S)
+        if kind == "v_rows_reversed":  # wrong key index into V
+            return P @ V[::-1]
+        if kind == "no_max_shift":
+            P = np.exp(S) / np.exp(S).sum(-1, keepdims=True)
+            P = P.astype(np.float16).astype(np.float32)
+        return P @ V
+
+    def prefill(q, k, v, causal, scale):
+        q, k, v = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
+        B, H, S, D_ = q.shape
+        out = np.empty((B, H, S, D_), dtype=np.float32)
+        for b in range(B):
+            for h in range(H):
+                out[b, h] = attn(q[b, h], k[b, h], v[b, h], scale, causal)
+        return out
+
+    return prefill
+
+
+@pytest.mark.parametrize("kind", ["scale_twice", "mask_edge", "v_rows_reversed", "scores_transposed", "no_max_shift"])
+def test_planted_prefill_mistakes_are_caught(kind):
+    with pytest.raises(AssertionError):
+        check_prefill_fn(_mutant_prefill(kind))
+
+
+@pytest.mark.parametrize("kind", ["no_clamp", "off_by_one_len"])
+def test_planted_decode_mistakes_are_caught(kind):
+    def bad_decode(q, k, v, lens, scale):
+        lens = np.asarray(lens).astype(np.int64)
+        if kind == "off_by_one_len":
+            lens = lens - 1
+        out = np.zeros((q.shape[0], q.shape[1], 1, D), dtype=np.float32)
+        for b in range(q.shape[0]):
+            n = int(lens[b]) if kind == "no_clamp" else int(min(lens[b], k.shape[2]))
+            if n <= 0:
+                continue
+            for h in range(q.shape[1]):
+                kk = k[b, h, :n].astype(np.float32)
+                if kind == "no_clamp" and n > k.shape[2]:
+                    kk = np.concatenate([kk, np.zeros((n - kk.shape[0], D), np.float32)])
+                vv = v[b, h, : kk.shape[0]].astype(np.float32)
+                if vv.shape[0] < kk.shape[0]:
+                    vv = np.concatenate([vv, np.zeros((kk.shape[0] - vv.shape[0], D), np.float32)])
+                out[b, h] = orc.attention_cpu(q[b, h].astype(np.float32), kk, vv, scale)
+        return out
+
+    with pytest.raises(AssertionError):
+        check_decode_fn(bad_decode)
