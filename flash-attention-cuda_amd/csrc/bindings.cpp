@@ -12,13 +12,13 @@
 // the fp32-output parity hooks `_prefill_fp32` / `_decode_fp32`.
 //
 // Torch-ROCm calls the HIP device "cuda", so `is_cuda()` is the right check
-// and the reference's messages stay verbatim.
+// and the reference's messages stay verbatim; the device guard and stream
+// lookup use torch's "masquerading as CUDA" HIP classes for the same reason.
 
 #include <torch/extension.h>
 
-#include <ATen/hip/HIPContext.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <cmath>
 #include <string>
@@ -47,7 +47,7 @@ void check_status(int rc) {
 
 void *stream_of(const at::Tensor &t) {
   return static_cast<void *>(
-      c10::hip::getCurrentHIPStream(t.device().index()).stream());
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
 }
 
 // bindings.cpp:10-27.
@@ -65,7 +65,7 @@ at::Tensor prefill_impl(const at::Tensor &q, const at::Tensor &k,
   TORCH_CHECK(q.size(2) > 0, "sequence length must be > 0");
   TORCH_CHECK(std::isfinite(scale), "scale must be finite");
 
-  const c10::hip::OptionalHIPGuard guard(q.device());
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
   at::Tensor o = out_f32 ? at::empty(q.sizes(), q.options().dtype(at::kFloat))
                          : at::empty_like(q);
   if (q.numel() == 0) return o;
@@ -131,7 +131,7 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
   TORCH_CHECK(split_size >= 0 && split_size <= (int64_t{1} << 30),
               "decode split size must be >= 0, got ", split_size);
 
-  const c10::hip::OptionalHIPGuard guard(q.device());
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
   at::Tensor o = out_f32 ? at::empty(q.sizes(), q.options().dtype(at::kFloat))
                          : at::empty_like(q);
   if (q.numel() == 0) return o;

@@ -172,7 +172,9 @@ def test_full_attention_key_permutation_invariance():
     a = flashattn_cuda._prefill_fp32(q.cuda(), k.cuda(), v.cuda(), False, SCALE)
     b = flashattn_cuda._prefill_fp32(q.cuda(), k[:, :, perm].contiguous().cuda(),
                                      v[:, :, perm].contiguous().cuda(), False, SCALE)
-    assert (a - b).abs().max().item() <= 1e-4
+    # Both runs are within BOUND of the same exact result; the tile-local
+    # fp16 roundings of P differ between the two key orders.
+    assert (a - b).abs().max().item() <= BOUND
 
 
 def test_negative_and_large_scales():
