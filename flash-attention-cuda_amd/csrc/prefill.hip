@@ -8,30 +8,33 @@
 // cores with fp32 accumulation.
 //
 // Work decomposition
-//   block  = 4 waves over 128 query rows of one (b, h): wave w owns the 64
-//            rows [64 (w % 2), +64) ("row group") and half w / 2 of the key
-//            tiles (even or odd 64-key tiles). The two halves merge their
-//            (m, l, O) states through LDS at the end. A wave covers 64 rows
-//            so that every K / V fragment it reads from LDS feeds two MFMAs
-//            (LDS bandwidth, not the matrix cores, bounds 32-row waves).
-//   CU     = two blocks (64 KiB LDS and <= 256 VGPRs each), so each SIMD runs
-//            two waves of independent blocks whose MFMA and softmax phases
-//            interleave.
+//   block  = 4 waves, 128 query rows of one (b, h); wave w owns rows
+//            [32 w, +32) and streams every 64-key tile its rows can see.
+//   CU     = two blocks (64 KiB LDS, <= 256 VGPRs each), so each SIMD runs
+//            two waves of independent blocks.
 //   grid   = one block per (b, h, 128-row query tile). With causal masking
 //            the work per block grows with the query tile; block b and block
 //            b + (number of CUs) share a CU, so the first CU-count blocks take
 //            the heaviest tiles in descending order and the rest the lightest
 //            in ascending order, pairing heavy with light work on every CU.
 //   tiles  = K and V stay row-major in LDS (16-byte chunks XOR-swizzled per
-//            row), double buffered per half and filled by direct global->LDS
-//            loads (global_load_lds_dwordx4) one tile pair ahead.
+//            row) in a 4-stage ring filled by direct global->LDS loads
+//            (global_load_lds_dwordx4) three tiles ahead of the MFMA work.
+//
+// Main-loop schedule (tiles that need no mask), per wave and 64-key tile t:
+//   barrier -> issue every LDS fragment read of V_t and K_{t+1} -> softmax of
+//   S_t on the VALU while those reads land -> PV(t) and QK(t+1) MFMAs
+//   interleaved as four independent accumulation chains. The MFMA burst runs
+//   at raised wave priority, so the other wave on the SIMD fills the VALU with
+//   its softmax meanwhile. S_t dies as P_t is formed, so one S buffer serves
+//   both tiles. Tiles that need a mask (causal diagonal, ragged tail) and
+//   query rows that see fewer than 512 keys take a plain per-tile step.
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
-//                 registers (two 32-row column groups per wave). Each lane
-//                 ends up with ONE query column per group and 16 of the 32
-//                 keys, so a query's softmax state lives in the lane pair
-//                 (l, l ^ 32).
+//                 registers. Each lane ends up with ONE query column and 16 of
+//                 the 32 keys, so a query's softmax state lives in the lane
+//                 pair (l, l ^ 32).
 //   O^T += V^T P^T : B = P^T straight from the S^T accumulators (fp32 -> fp16
 //                 pack), A = V^T read with ds_read_b64_tr_b16: inside each
 //                 16-lane group, lane j receives element e from source lane
@@ -61,17 +64,21 @@
 namespace fa {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * kWave;      // 256
-constexpr int kRowsPerWave = 64;              // two 32-row column groups
-constexpr int kBr = 2 * kRowsPerWave;         // 128 query rows per block
+constexpr int kQWaves = 4;                    // row waves per key half
+constexpr int kThreads = 2 * kQWaves * kWave; // 512: two key halves
+constexpr int kRowsPerWave = 32;
+constexpr int kBr = kQWaves * kRowsPerWave;   // 128 query rows per block
 constexpr int kBc = 64;                       // keys per tile
 constexpr int kTileHalves = kBc * kHeadDim;   // 4096 halves = 8 KiB
-constexpr int kStages = 2;
+constexpr int kStages = 4;
+constexpr int kAhead = kStages - 1;           // tiles in flight ahead of use
+constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per tile
 constexpr int kSplitPRowsBelow = 512;  // rows with fewer keys than this: split P
 constexpr float kNegHuge = -3.0e38f;
+// s_waitcnt immediate for vmcnt(0) with expcnt / lgkmcnt left unconstrained.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
-// LDS: [half][stage][K | V][64 rows x 64 halves] = 64 KiB
+// LDS: [key half][stage][K | V][64 rows x 64 halves] = 128 KiB
 constexpr int kStageHalves = 2 * kTileHalves;
 constexpr int kHalfHalves = kStages * kStageHalves;
 constexpr int kLdsHalves = 2 * kHalfHalves;
@@ -91,37 +98,52 @@ __device__ __forceinline__ int k_swz(int row) {
 }
 __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
 
-// Issue the direct global->LDS loads of one 64-key K tile and V tile for one
-// half (128 threads, 8 x 16 B each). Rows past the sequence end are clamped
-// to the last row: they are masked in the softmax (K) and weighted by 0 (V).
+// One direct global->LDS load: 16 bytes per lane from `src` to LDS address
+// m0 + 16 * lane. Written in asm so the compiler does not treat later LDS
+// reads of other stages as possibly aliasing the in-flight write (it would
+// otherwise wait for every outstanding load before each of them); the ring
+// tracks completion itself with explicit vmcnt waits.
+__device__ __forceinline__ void global_to_lds16(const void *src, const void *lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(lds_dst))));
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(m0)
+      : "memory", "m0");
+}
+
+// Issue the direct global->LDS loads of one 64-key K tile and V tile
+// (256 threads, 4 x 16 B each). Rows past the sequence end are clamped to the
+// last row: they are masked in the softmax (K) and weighted by 0 (V).
 __device__ __forceinline__ void issue_tile_loads(const _Float16 *__restrict__ kp,
                                                  const _Float16 *__restrict__ vp,
                                                  _Float16 *stage_lds, int key0,
-                                                 int seq, int htid) {
-  const int lane = htid & 63;
-  const int w = htid >> 6;  // wave within the half, 0..1
+                                                 int seq, int tid) {
+  const int lane = tid & 63;
+  const int w = tid >> 6;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int rblock = (w * 4 + it) * 8;  // 8 rows per wave instruction
+  for (int it = 0; it < 2; ++it) {
+    const int rblock = (w * 2 + it) * 8;  // 8 rows per wave instruction
     const int r = rblock + (lane >> 3);
     const int p = lane & 7;
     const int key = min(key0 + r, seq - 1);
     const size_t row_off = static_cast<size_t>(key) * kHeadDim;
-    __builtin_amdgcn_global_load_lds(kp + row_off + ((p ^ k_swz(r)) << 3),
-                                     (lds_void *)(stage_lds + rblock * kHeadDim),
-                                     16, 0, 0);
-    __builtin_amdgcn_global_load_lds(
-        vp + row_off + ((p ^ v_swz(r)) << 3),
-        (lds_void *)(stage_lds + kTileHalves + rblock * kHeadDim), 16, 0, 0);
+    global_to_lds16(kp + row_off + ((p ^ k_swz(r)) << 3), stage_lds + rblock * kHeadDim);
+    global_to_lds16(vp + row_off + ((p ^ v_swz(r)) << 3),
+                    stage_lds + kTileHalves + rblock * kHeadDim);
   }
 }
 
-// Make this thread's global->LDS loads complete, then synchronise the block.
-// A plain s_barrier: __syncthreads() would add a release fence, which drains
-// every outstanding memory operation.
-__device__ __forceinline__ void loads_done_barrier() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
+// Wait until at most N of this thread's global->LDS loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  if constexpr (N == 0)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
@@ -134,11 +156,10 @@ __device__ __forceinline__ half4 lds_tr16(const _Float16 *p) {
   return __builtin_bit_cast(half4, r);
 }
 
-// Softmax state of the two 32-row column groups a wave owns.
 struct SoftmaxState {
-  float m[2];       // running max per group (log2 domain, scaled by c)
-  float l[2];       // this lane's share of each row sum
-  floatx16 o[2][2]; // O^T accumulators [group][d-block]
+  float m;       // running max (log2 domain, already scaled by c)
+  float l;       // this lane's share of the row sum
+  floatx16 o[2]; // O^T accumulators: d-blocks 0 and 1
 };
 
 // Per-lane LDS offsets (in halves, relative to a stage) of every fragment a
@@ -167,6 +188,41 @@ __device__ __forceinline__ FragOffsets frag_offsets(int lane) {
   return f;
 }
 
+// Register copies of the LDS fragments one tile step consumes.
+struct KFrags { half8 f[2][4]; };  // [32-key block][d-step]
+struct VFrags { half8 f[4][2]; };  // [16-key step][d-block]
+
+__device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
+                                       const FragOffsets &fo, KFrags &k) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) k.f[kb][s] = lds_b128(tile + fo.k[s] + kb * 32 * kHeadDim);
+}
+
+__device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
+                                       const FragOffsets &fo, VFrags &v) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int kb = ks >> 1, h = ks & 1;
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        const int row_off = (kb * 32 + 16 * h + 8 * part) * kHeadDim;
+        const half4 v4 = lds_tr16(tile + fo.v[db] + row_off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v.f[ks][db][4 * part + e] = v4[e];
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
+                                         const floatx16 &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 // max(x[l], x[l ^ 32]) for every lane: one v_permlane32_swap (VALU), no LDS.
 // With both operands holding x, the swap leaves lanes 0-31 of the first
 // register and lanes 32-63 of the second unchanged and exchanges the other
@@ -184,56 +240,14 @@ __device__ __forceinline__ float max_lane_pair(float x) {
   return a;
 }
 
-// S^T = K Q^T for one 64-key tile and both row groups: every K fragment
-// feeds two MFMAs.
-__device__ __forceinline__ void qk_tile(const _Float16 *__restrict__ tile,
-                                        const FragOffsets &f,
-                                        const half8 (&qf)[2][4],
-                                        floatx16 (&s_acc)[2][2]) {
-#pragma unroll
-  for (int gq = 0; gq < 2; ++gq)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) s_acc[gq][kb][a] = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const half8 kf = lds_b128(tile + f.k[s] + kb * 32 * kHeadDim);
-#pragma unroll
-      for (int gq = 0; gq < 2; ++gq)
-        s_acc[gq][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[gq][s],
-                                                              s_acc[gq][kb], 0, 0, 0);
-    }
-  }
-}
-
-// S^T = K Q^T for one 64-key tile and one row group (slow path).
-__device__ __forceinline__ void qk_group(const _Float16 *__restrict__ tile,
-                                         const FragOffsets &f, const half8 (&qf)[4],
-                                         floatx16 (&s_acc)[2]) {
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int a = 0; a < 16; ++a) s_acc[kb][a] = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      s_acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-          lds_b128(tile + f.k[s] + kb * 32 * kHeadDim), qf[s], s_acc[kb], 0, 0, 0);
-}
-
-// Online softmax of one S^T tile for one row group, producing P^T fragments.
+// Online softmax of one S^T tile, producing P^T fragments (hi [+ lo]).
 // MASK: keys past the end or above the causal diagonal;
 // SPLIT: P feeds the PV product as hi + lo fp16 parts.
 template <bool CAUSAL, bool MASK, bool SPLIT>
-__device__ __forceinline__ void softmax_group(floatx16 (&s_acc)[2], int key0,
-                                              int seq, int my_q, int lane,
-                                              float c_scale, float &m, float &l,
-                                              floatx16 (&o)[2], half8 (&p_hi)[4],
-                                              half8 (&p_lo)[4]) {
+__device__ __forceinline__ void softmax_tile(floatx16 (&s_acc)[2], int key0, int seq,
+                                             int my_q, int lane, float c_scale,
+                                             SoftmaxState &st, half8 (&p_hi)[4],
+                                             half8 (&p_lo)[4]) {
   // Element a of key block kb holds key key0 + kb*32 + 8 (a/4) + 4 g + a%4;
   // it is visible iff that offset is <= lim (last visible key - key0 - 4 g).
   const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
@@ -249,18 +263,18 @@ __device__ __forceinline__ void softmax_group(floatx16 (&s_acc)[2], int key0,
   }
   mx = max_lane_pair(mx);
   const float mx_scaled = mx * c_scale;
-  const bool raise = mx_scaled > m;
+  const bool raise = mx_scaled > st.m;
   if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-    const float m_new = raise ? mx_scaled : m;
-    const float alpha = fast_exp2(m - m_new);
-    m = m_new;
-    l *= alpha;
+    const float m_new = raise ? mx_scaled : st.m;
+    const float alpha = fast_exp2(st.m - m_new);
+    st.m = m_new;
+    st.l *= alpha;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int a = 0; a < 16; ++a) o[db][a] *= alpha;
+      for (int a = 0; a < 16; ++a) st.o[db][a] *= alpha;
   }
-  const float m_use = m;
+  const float m_use = st.m;
 
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   float lsum = 0.f;
@@ -288,255 +302,268 @@ __device__ __forceinline__ void softmax_group(floatx16 (&s_acc)[2], int key0,
       }
     }
   }
-  l += lsum;
+  st.l += lsum;
 }
 
-// O^T += V^T P^T for one 64-key tile and both row groups: every V^T
-// fragment feeds two MFMAs.
-template <bool SPLIT>
-__device__ __forceinline__ void pv_tile(const _Float16 *__restrict__ tile,
-                                        const FragOffsets &f,
-                                        const half8 (&p_hi)[2][4],
-                                        const half8 (&p_lo)[2][4],
-                                        SoftmaxState &st) {
+// PV(t) and QK(t+1) as four independent accumulation chains (O d-blocks 0/1,
+// S key-blocks 0/1), issued alternately.
+template <bool WITH_QK>
+__device__ __forceinline__ void pv_qk_mfma(const VFrags &v, const half8 (&p)[4],
+                                           const KFrags &k, const half8 (&qf)[4],
+                                           floatx16 (&o)[2], floatx16 (&s)[2]) {
+  if (WITH_QK) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int kb = ks >> 1, h = ks & 1;
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
-      half8 vf;
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        const int row_off = (kb * 32 + 16 * h + 8 * part) * kHeadDim;
-        const half4 v4 = lds_tr16(tile + f.v[db] + row_off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vf[4 * part + e] = v4[e];
-      }
-#pragma unroll
-      for (int gq = 0; gq < 2; ++gq) {
-        st.o[gq][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p_hi[gq][ks],
-                                                             st.o[gq][db], 0, 0, 0);
-        if (SPLIT)
-          st.o[gq][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p_lo[gq][ks],
-                                                               st.o[gq][db], 0, 0, 0);
-      }
+      o[db] = mfma(v.f[i][db], p[i], o[db]);
+      if (WITH_QK) s[db] = mfma(k.f[db][i], qf[i], s[db]);
     }
   }
 }
 
-// O^T += V^T P^T for one row group with P split into hi + lo parts (the
-// rare masked / short-row path; V fragments are read once per group there to
-// keep the live P registers of only one group).
-__device__ __forceinline__ void pv_group_split(const _Float16 *__restrict__ tile,
-                                               const FragOffsets &f,
-                                               const half8 (&p_hi)[4],
-                                               const half8 (&p_lo)[4],
-                                               floatx16 (&o)[2]) {
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int kb = ks >> 1, h = ks & 1;
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      half8 vf;
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        const int row_off = (kb * 32 + 16 * h + 8 * part) * kHeadDim;
-        const half4 v4 = lds_tr16(tile + f.v[db] + row_off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vf[4 * part + e] = v4[e];
-      }
-      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p_hi[ks], o[db], 0, 0, 0);
-      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p_lo[ks], o[db], 0, 0, 0);
-    }
-  }
-}
-
-// One 64-key tile for one wave. Fast path: QK, softmax of both row groups,
-// PV with shared K / V fragments. Masked / short-row path: QK, softmax and
-// split-P PV one row group at a time (fewer live registers).
-template <bool CAUSAL, bool SLOW>
-__device__ __forceinline__ void tile_step(const _Float16 *__restrict__ tile,
-                                          const FragOffsets &f,
-                                          const half8 (&qf)[2][4], int key0,
-                                          int seq, int row0, int lane,
+// Plain (non-pipelined) step for masked / short-row tiles: QK, softmax with
+// mask and split P, PV issued twice.
+template <bool CAUSAL>
+__device__ __forceinline__ void slow_step(const _Float16 *__restrict__ tile,
+                                          const FragOffsets &fo, const half8 (&qf)[4],
+                                          int key0, int seq, int my_q, int lane,
                                           float c_scale, SoftmaxState &st) {
-  if (!SLOW) {
-    floatx16 s_acc[2][2];
-    qk_tile(tile, f, qf, s_acc);
-    half8 p_hi[2][4], p_unused[2][4];
+  KFrags k;
+  VFrags v;
+  read_k(tile, fo, k);
+  read_v(tile, fo, v);
+  floatx16 s[2];
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq)
-      softmax_group<CAUSAL, false, false>(s_acc[gq], key0, seq,
-                                          row0 + 32 * gq + (lane & 31), lane,
-                                          c_scale, st.m[gq], st.l[gq], st.o[gq],
-                                          p_hi[gq], p_unused[gq]);
-    pv_tile<false>(tile, f, p_hi, p_unused, st);
-  } else {
+  for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
-      floatx16 s_acc[2];
-      half8 p_hi[4], p_lo[4];
-      qk_group(tile, f, qf[gq], s_acc);
-      softmax_group<CAUSAL, true, true>(s_acc, key0, seq,
-                                        row0 + 32 * gq + (lane & 31), lane,
-                                        c_scale, st.m[gq], st.l[gq], st.o[gq],
-                                        p_hi, p_lo);
-      pv_group_split(tile, f, p_hi, p_lo, st.o[gq]);
+    for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
+  }
+  half8 p_hi[4], p_lo[4];
+  softmax_tile<CAUSAL, true, true>(s, key0, seq, my_q, lane, c_scale, st, p_hi, p_lo);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      st.o[db] = mfma(v.f[i][db], p_hi[i], st.o[db]);
+      st.o[db] = mfma(v.f[i][db], p_lo[i], st.o[db]);
     }
   }
 }
+
+// Tile ring of one key half: half h owns tiles 2k + h (k = 0, 1, ...), stage
+// k % kStages of its LDS region.
+struct HalfRing {
+  _Float16 *lds;
+  const _Float16 *kp, *vp;
+  int seq, n_tiles, half, htid;
+
+  __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
+  __device__ __forceinline__ _Float16 *stage(int k) const {
+    return lds + (k & (kStages - 1)) * kStageHalves;
+  }
+  __device__ __forceinline__ void issue(int k) const {
+    if (tile(k) < n_tiles) issue_tile_loads(kp, vp, stage(k), tile(k) * kBc, seq, htid);
+  }
+  // Start of step k: this half's tiles k and k+1 are resident and visible to
+  // the whole block, then the load of its tile k + kAhead is issued into the
+  // stage tile k-1 used (every wave finished reading it before the barrier).
+  // A plain s_barrier: __syncthreads() would add a release fence, which
+  // drains every outstanding load of the ring.
+  __device__ __forceinline__ void advance(int k) const {
+    if (tile(k + 2) < n_tiles)
+      wait_loads<kLoadsPerTile>();
+    else
+      wait_loads<0>();
+    __builtin_amdgcn_s_barrier();
+    issue(k + kAhead);
+  }
+};
 
 template <bool CAUSAL, bool OUT_F32>
-__global__ __launch_bounds__(kThreads, 2) void prefill_kernel(
+__global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
-    int n_qtiles, int n_cu, float c_scale, bool negate_q) {
+    int n_qtiles, float c_scale, bool negate_q) {
   __shared__ __attribute__((aligned(1024))) _Float16 lds[kLdsHalves];
 
-  // Block -> (query tile, head). Rank 0 is the heaviest tile. While the grid
-  // fits in two blocks per CU, block b and block b + n_cu share a CU: ranks
-  // ascend over the first n_cu blocks and descend over the rest.
-  const int nb = static_cast<int>(gridDim.x);
-  const int b = static_cast<int>(blockIdx.x);
-  const int rank = (CAUSAL && nb <= 2 * n_cu && b >= n_cu) ? nb - 1 - (b - n_cu) : b;
-  const int bh_count = nb / n_qtiles;
-  const int qtile = n_qtiles - 1 - rank / bh_count;
-  const int bh = rank % bh_count;
+  // Heaviest (last) query tiles first: one block fills a CU, so dispatching
+  // in decreasing work order is a longest-first list schedule.
+  const int bh_count = static_cast<int>(gridDim.x) / n_qtiles;
+  const int qtile = n_qtiles - 1 - static_cast<int>(blockIdx.x) / bh_count;
+  const int bh = static_cast<int>(blockIdx.x) % bh_count;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int rg = wave & 1;    // row group of this wave
-  const int half = wave >> 1; // 0: even key tiles, 1: odd key tiles
-  const int htid = tid & 127;
+  const int rw = wave & (kQWaves - 1);  // row wave: rows [32 rw, +32)
+  const int half = wave / kQWaves;      // key half: tiles 2k + half
+  const int htid = tid & (kQWaves * kWave - 1);
   const int col = lane & 31;
   const int g = lane >> 5;
 
   const size_t head_off = static_cast<size_t>(bh) * seq * kHeadDim;
   const _Float16 *qp = q + head_off;
-  const _Float16 *kp = k + head_off;
-  const _Float16 *vp = v + head_off;
 
   const int q0 = qtile * kBr;
-  const int row0 = q0 + rg * kRowsPerWave;  // first query row of this wave
-
-  // Q^T fragments: group gq, lane holds query row0 + 32 gq + col, head dims
-  // [32 g + 8 s, +8).
-  half8 qf[2][4];
-#pragma unroll
-  for (int gq = 0; gq < 2; ++gq) {
-    const int my_q = row0 + 32 * gq + col;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (my_q < seq) {
-        qf[gq][s] = *reinterpret_cast<const half8 *>(
-            qp + static_cast<size_t>(my_q) * kHeadDim + 32 * g + 8 * s);
-        if (negate_q) qf[gq][s] = -qf[gq][s];
-      } else {
-        qf[gq][s] = half8{};
-      }
-    }
-  }
+  const int qw0 = q0 + rw * kRowsPerWave;
+  const int my_q = qw0 + col;
 
   const int key_end = CAUSAL ? min(seq, q0 + kBr) : seq;
   const int n_tiles = (key_end + kBc - 1) / kBc;
-  const int n_pairs = (n_tiles + 1) / 2;
-  // Keys this wave can see; tiles past them are skipped.
-  const int wave_key_end = CAUSAL ? min(seq, row0 + kRowsPerWave) : seq;
-  // Tiles below main_end need no mask for any row of the block and all its
-  // rows see >= kSplitPRowsBelow keys: plain fast path.
+  HalfRing ring{lds + half * kHalfHalves, k + head_off, v + head_off, seq, n_tiles,
+                half, htid};
+  const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
+  // Tiles [0, 2 n_main) need no mask for any wave of the block and all its
+  // rows see >= kSplitPRowsBelow keys: each half runs n_main pipelined steps
+  // on them. The rest (causal diagonal, ragged tail, short rows) take the
+  // plain masked step.
   const bool short_rows = CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow;
-  const int main_end = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
+  const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
+  const int n_main = main_tiles / 2;
+  const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
+
+#pragma unroll
+  for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
+
+  // Q^T fragments: lane holds query my_q, head dims [32 g + 8 s, +8).
+  half8 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (my_q < seq) {
+      qf[s] = *reinterpret_cast<const half8 *>(
+          qp + static_cast<size_t>(my_q) * kHeadDim + 32 * g + 8 * s);
+      if (negate_q) qf[s] = -qf[s];
+    } else {
+      qf[s] = half8{};
+    }
+  }
+  // One wait the compiler can see (it cannot see the ring's asm waits): Q and
+  // the first kAhead tiles are resident, and no compiler-issued load is
+  // pending inside the loops, so it adds no vmcnt waits there.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __builtin_amdgcn_s_barrier();
+  ring.issue(kAhead);
 
   const FragOffsets fo = frag_offsets(lane);
   SoftmaxState st;
+  st.m = kNegHuge;
+  st.l = 0.f;
 #pragma unroll
-  for (int gq = 0; gq < 2; ++gq) {
-    st.m[gq] = kNegHuge;
-    st.l[gq] = 0.f;
+  for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int a = 0; a < 16; ++a) st.o[db][a] = 0.f;
+
+  // ---- pipelined main loop, ping-pong between the halves --------------------
+  // Step kk, half 0: softmax S(kk) -> burst [PV(kk), QK(kk+1)].
+  //          half 1: burst [PV(kk), QK(kk+1)] -> softmax S(kk+1).
+  // The two waves sharing a SIMD (same row wave, different half) are thus in
+  // opposite phases: one issues MFMAs while the other runs the exp-heavy
+  // softmax. The burst runs at raised priority so its MFMAs issue first.
+  floatx16 s_acc[2];
+  KFrags kf;
+  VFrags vf;
+  half8 p_hi[4], p_lo[4];
+  if (n_main > 0) {
+    read_k(ring.stage(0), fo, kf);
 #pragma unroll
-      for (int a = 0; a < 16; ++a) st.o[gq][db][a] = 0.f;
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a) s_acc[kb][a] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_acc[kb] = mfma(kf.f[kb][i], qf[i], s_acc[kb]);
+    }
+    if (half == 1)
+      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(0) * kBc, seq, my_q, lane,
+                                         c_scale, st, p_hi, p_lo);
+  }
+  int kk = 0;
+  for (; kk < n_main; ++kk) {
+    if (kk > 0) ring.advance(kk);
+    // QK(kk+1) is issued unconditionally: on the last main step it reads
+    // whatever stage kk+1 holds (in bounds) and the result is discarded,
+    // which keeps the accumulators in place (a branch makes the compiler
+    // copy them every step).
+    read_v(ring.stage(kk), fo, vf);
+    read_k(ring.stage(kk + 1), fo, kf);
+    if (half == 0)
+      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(kk) * kBc, seq, my_q,
+                                         lane, c_scale, st, p_hi, p_lo);
+    __builtin_amdgcn_s_setprio(2);
+    pv_qk_mfma<true>(vf, p_hi, kf, qf, st.o, s_acc);
+    __builtin_amdgcn_s_setprio(0);
+    if (half == 1 && kk + 1 < n_main)
+      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(kk + 1) * kBc, seq, my_q,
+                                         lane, c_scale, st, p_hi, p_lo);
   }
 
-  _Float16 *my_lds = lds + half * kHalfHalves;
-  if (half * kBc < key_end)
-    issue_tile_loads(kp, vp, my_lds, half * kBc, seq, htid);
-  loads_done_barrier();
-
-  for (int j = 0; j < n_pairs; ++j) {
-    const int next_key0 = (2 * (j + 1) + half) * kBc;
-    if (next_key0 < key_end)
-      issue_tile_loads(kp, vp, my_lds + ((j + 1) & 1) * kStageHalves, next_key0,
-                       seq, htid);
-    const int t = 2 * j + half;
-    const int key0 = t * kBc;
-    if (key0 < wave_key_end) {
-      const _Float16 *tile = my_lds + (j & 1) * kStageHalves;
-      if (t < main_end)
-        tile_step<CAUSAL, false>(tile, fo, qf, key0, seq, row0, lane, c_scale, st);
-      else
-        tile_step<CAUSAL, true>(tile, fo, qf, key0, seq, row0, lane, c_scale, st);
-    }
-    loads_done_barrier();
+  // ---- masked / short-row tiles: one plain step per tile ---------------------
+  for (; kk < n_steps; ++kk) {
+    if (kk > 0) ring.advance(kk);
+    const int key0 = ring.tile(kk) * kBc;
+    if (key0 < wave_key_end)
+      slow_step<CAUSAL>(ring.stage(kk), fo, qf, key0, seq, my_q, lane, c_scale, st);
   }
 
   // ---- merge the two halves through LDS, normalise, store ------------------
-  // Layout: [row group][68 values][64 lanes] fp32 (reuses the tile buffers;
-  // the barrier above ended every read of them).
-  float *xchg = reinterpret_cast<float *>(lds) + rg * (68 * kWave) + lane;
+  // Layout: [row wave][34 values][64 lanes] fp32, reusing the tile buffers.
+  // Every load the ring issued has completed (the last steps waited with
+  // vmcnt(0)); the barrier ends every read of the tiles.
+  wait_loads<0>();
+  __builtin_amdgcn_s_barrier();
+  float *xchg = reinterpret_cast<float *>(lds) + rw * (34 * kWave) + lane;
   if (half == 1) {
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int a = 0; a < 16; ++a)
-          xchg[(32 * gq + 16 * db + a) * kWave] = st.o[gq][db][a];
-      xchg[(64 + gq) * kWave] = st.m[gq];
-      xchg[(66 + gq) * kWave] = st.l[gq];
-    }
+      for (int a = 0; a < 16; ++a) xchg[(16 * db + a) * kWave] = st.o[db][a];
+    xchg[32 * kWave] = st.m;
+    xchg[33 * kWave] = st.l;
   }
   __syncthreads();
   if (half == 1) return;
-
-#pragma unroll
-  for (int gq = 0; gq < 2; ++gq) {
-    const float m1 = xchg[(64 + gq) * kWave];
-    const float l1 = xchg[(66 + gq) * kWave];
-    const float m = fmaxf(st.m[gq], m1);
-    const float f0 = fast_exp2(st.m[gq] - m);
+  {
+    const float m1 = xchg[32 * kWave];
+    const float l1 = xchg[33 * kWave];
+    const float m = fmaxf(st.m, m1);
+    const float f0 = fast_exp2(st.m - m);
     const float f1 = fast_exp2(m1 - m);
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a)
-        st.o[gq][db][a] =
-            st.o[gq][db][a] * f0 + xchg[(32 * gq + 16 * db + a) * kWave] * f1;
-    const float l_own = st.l[gq] * f0 + l1 * f1;
-    const float l_tot = l_own + __shfl_xor(l_own, 32);
-    const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-    const int my_q = row0 + 32 * gq + col;
-    if (my_q < seq) {
-      const size_t row_off = head_off + static_cast<size_t>(my_q) * kHeadDim;
+        st.o[db][a] = st.o[db][a] * f0 + xchg[(16 * db + a) * kWave] * f1;
+    st.l = st.l * f0 + l1 * f1;
+  }
+
+  // ---- epilogue: O = O^T / l, one query row per lane -------------------------
+  const float l_tot = st.l + __shfl_xor(st.l, 32);
+  const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+  if (my_q < seq) {
+    const size_t row_off = head_off + static_cast<size_t>(my_q) * kHeadDim;
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
+    for (int db = 0; db < 2; ++db) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int d = db * 32 + 8 * jj + 4 * g;  // 4 consecutive dims
-          if (OUT_F32) {
-            floatx4 r;
+      for (int jj = 0; jj < 4; ++jj) {
+        const int d = db * 32 + 8 * jj + 4 * g;  // 4 consecutive dims
+        if (OUT_F32) {
+          floatx4 r;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = st.o[gq][db][4 * jj + e] * inv_l;
-            *reinterpret_cast<floatx4 *>(static_cast<float *>(o) + row_off + d) = r;
-          } else {
-            half4 r;
+          for (int e = 0; e < 4; ++e) r[e] = st.o[db][4 * jj + e] * inv_l;
+          *reinterpret_cast<floatx4 *>(static_cast<float *>(o) + row_off + d) = r;
+        } else {
+          half4 r;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              r[e] = static_cast<_Float16>(st.o[gq][db][4 * jj + e] * inv_l);
-            *reinterpret_cast<half4 *>(static_cast<_Float16 *>(o) + row_off + d) = r;
-          }
+          for (int e = 0; e < 4; ++e)
+            r[e] = static_cast<_Float16>(st.o[db][4 * jj + e] * inv_l);
+          *reinterpret_cast<half4 *>(static_cast<_Float16 *>(o) + row_off + d) = r;
         }
       }
     }
@@ -545,15 +572,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(
 
 template <bool CAUSAL, bool OUT_F32>
 void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
-                int seq, int n_cu, float c_scale, bool negate_q,
-                hipStream_t stream) {
+                int seq, float c_scale, bool negate_q, hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
   const unsigned blocks = static_cast<unsigned>(bh) * n_qtiles;
   hipLaunchKernelGGL((prefill_kernel<CAUSAL, OUT_F32>), dim3(blocks),
                      dim3(kThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
-                     static_cast<const _Float16 *>(v), o, seq, n_qtiles, n_cu,
+                     static_cast<const _Float16 *>(v), o, seq, n_qtiles,
                      c_scale, negate_q);
 }
 
@@ -565,20 +591,16 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
   const int bh = batch * heads;
   const float c_scale = fabsf(scale) * kLog2e;
   const bool negate_q = scale < 0.f;
-  int dev = 0;
-  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
-  if (rc != FA_OK) return rc;
-  const int n_cu = device_cu_count(dev) > 0 ? device_cu_count(dev) : 1;
   if (causal) {
     if (out_f32)
-      launch_one<true, true>(q, k, v, o, bh, seq, n_cu, c_scale, negate_q, stream);
+      launch_one<true, true>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
     else
-      launch_one<true, false>(q, k, v, o, bh, seq, n_cu, c_scale, negate_q, stream);
+      launch_one<true, false>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
   } else {
     if (out_f32)
-      launch_one<false, true>(q, k, v, o, bh, seq, n_cu, c_scale, negate_q, stream);
+      launch_one<false, true>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
     else
-      launch_one<false, false>(q, k, v, o, bh, seq, n_cu, c_scale, negate_q, stream);
+      launch_one<false, false>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
   }
   return check_hip(hipGetLastError(), "prefill_kernel launch");
 }
