@@ -1,6 +1,7 @@
 """Benchmark of the MI355X FlashAttention hot path (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-configs]
+                    [--only all|prefill|decode|copy]
 
 Prints ONE JSON line on stdout (everything else goes to stderr):
 
@@ -166,9 +167,10 @@ def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, war
 
 
 def cpu_baseline(budget_s=12.0):
-    """The CPU oracle on a bounded sample of config 3: causal heads of
-    B=1, S=4096 one at a time (one warm-up head, then heads until the budget
-    is spent), in TFLOP/s by the same causal FLOP convention."""
+    """The CPU oracle on a bounded sample of config 3: the 14 causal heads of
+    B=1, S=4096 one at a time, cycling over them (one warm-up head first)
+    until at least `budget_s` seconds of work are done, in TFLOP/s by the same
+    causal FLOP convention."""
     import numpy as np
 
     from oracle import attention as orc
@@ -183,10 +185,11 @@ def cpu_baseline(budget_s=12.0):
     orc.attention_cpu(q[0, 0], k[0, 0], v[0, 0], SCALE, True)  # warm-up
     t0 = time.perf_counter()
     done = 0
-    while done < 14:
-        orc.attention_cpu(q[0, done], k[0, done], v[0, done], SCALE, True)
+    while True:
+        h = done % 14
+        orc.attention_cpu(q[0, h], k[0, h], v[0, h], SCALE, True)
         done += 1
-        if time.perf_counter() - t0 > budget_s:
+        if time.perf_counter() - t0 >= budget_s:
             break
     dt = time.perf_counter() - t0
     flops = attention_flops(1, done, 4096, True)
@@ -196,11 +199,28 @@ def cpu_baseline(budget_s=12.0):
         "cores": int(blas_threads),
         "host_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
-        "sample": f"config 3 (causal S=4096, D=64), {done} of 14 heads, fp32 numpy "
-                  f"restatement of src/attention_cpu.py with a causal mask, "
-                  f"{dt:.2f} s after one warm-up head",
+        "sample": f"config 3 (causal S=4096, D=64): {done} head-passes cycling over its "
+                  f"14 heads, fp32 numpy restatement of src/attention_cpu.py with a "
+                  f"causal mask, {dt:.2f} s after one warm-up head",
         "seconds_per_head": dt / done,
     }
+
+
+def copy_calibration(steps):
+    """A plain 1 GiB device-to-device copy, `steps` times: the known-size
+    kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters into HBM
+    bytes (it reads and writes exactly 1 GiB per launch)."""
+    import torch
+
+    n = 1 << 29  # fp16 elements = 1 GiB
+    src = torch.randn(n, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    step_ms, kern_ms = timed_steps([lambda: dst.copy_(src)], steps, 1)
+    nbytes = 2 * src.numel() * 2
+    return {"bytes_per_launch": nbytes, "kernel_ms": kern_ms,
+            "gbs": nbytes / (kern_ms * 1e-3) / 1e9}
 
 
 def load_traffic(name):
@@ -221,7 +241,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config sweep")
-    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy"], default="all",
+                    help="copy: only the 1 GiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -240,6 +261,13 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} ({props.multi_processor_count} CUs), "
         f"arch {getattr(props, 'gcnArchName', '?')}")
+
+    if args.only == "copy":
+        c = copy_calibration(args.steps)
+        log(f"1 GiB copy: {c['kernel_ms'] * 1e3:.1f} us, {c['gbs']:.1f} GB/s (read + write)")
+        print(json.dumps({"metric": "device copy GB/s (counter calibration)",
+                          "value": c["gbs"], "unit": "GB/s", **c}), flush=True)
+        return
 
     result = {
         "metric": "prefill TFLOP/s & %MFMA peak @S=4096; decode KV GB/s & %HBM peak",
