@@ -8,27 +8,32 @@
 // cores with fp32 accumulation.
 //
 // Work decomposition
-//   block  = 4 waves, 128 query rows of one (b, h); wave w owns rows
-//            [32 w, +32) and streams every 64-key tile its rows can see.
-//   CU     = two blocks (64 KiB LDS, <= 256 VGPRs each), so each SIMD runs
-//            two waves of independent blocks.
-//   grid   = one block per (b, h, 128-row query tile). With causal masking
-//            the work per block grows with the query tile; block b and block
-//            b + (number of CUs) share a CU, so the first CU-count blocks take
-//            the heaviest tiles in descending order and the rest the lightest
-//            in ascending order, pairing heavy with light work on every CU.
+//   block  = 8 waves, 128 query rows of one (b, h): 4 row waves x 2 key
+//            halves. Row wave r owns rows [32 r, +32); key half h streams the
+//            64-key tiles 2 k + h its rows can see. The two halves keep
+//            separate online-softmax states and merge them through LDS at the
+//            end, so a block's critical path is half its key range.
+//   CU     = one block (128 KiB LDS, <= 256 VGPRs per lane): each SIMD runs
+//            the two waves of one row wave, one per key half.
+//   grid   = one block per (b, h, 128-row query tile), heaviest (last) query
+//            tiles first: with causal masking the work per block grows with
+//            the query tile, and dispatching in decreasing work order is a
+//            longest-first list schedule over the CUs.
 //   tiles  = K and V stay row-major in LDS (16-byte chunks XOR-swizzled per
-//            row) in a 4-stage ring filled by direct global->LDS loads
-//            (global_load_lds_dwordx4) three tiles ahead of the MFMA work.
+//            row), in one 4-stage ring per key half filled by direct
+//            global->LDS loads (global_load_lds_dwordx4) three of that half's
+//            tiles ahead of the MFMA work.
 //
-// Main-loop schedule (tiles that need no mask), per wave and 64-key tile t:
-//   barrier -> issue every LDS fragment read of V_t and K_{t+1} -> softmax of
-//   S_t on the VALU while those reads land -> PV(t) and QK(t+1) MFMAs
-//   interleaved as four independent accumulation chains. The MFMA burst runs
-//   at raised wave priority, so the other wave on the SIMD fills the VALU with
-//   its softmax meanwhile. S_t dies as P_t is formed, so one S buffer serves
-//   both tiles. Tiles that need a mask (causal diagonal, ragged tail) and
-//   query rows that see fewer than 512 keys take a plain per-tile step.
+// Main-loop schedule (tiles that need no mask), per wave and step k:
+//   barrier -> issue every LDS fragment read of V and of the next K tile ->
+//   half 0: softmax of S_k, then the burst PV(k) + QK(k+1);
+//   half 1: the burst PV(k) + QK(k+1), then the softmax of S_{k+1}.
+//   The burst interleaves four independent MFMA accumulation chains and runs
+//   at raised wave priority. The two waves that share a SIMD are therefore in
+//   opposite phases: one issues MFMAs while the other runs its exp-heavy
+//   softmax on the VALU. S dies as P is formed, so one S buffer serves both
+//   tiles. Tiles that need a mask (causal diagonal, ragged tail) and query
+//   rows that see fewer than 512 keys take a plain per-tile step.
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
