@@ -44,6 +44,10 @@ HIPCC_FLAGS = [
     # Packed-FP32 VALU forms (v_pk_fma_f32 & co.) are kept out of the device
     # code; the host pass prints a harmless "not a recognized feature" note.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the prefill rescales and reads its O and S
+    # accumulators with VALU ops, which cannot address AGPRs directly; the
+    # AGPRs hold the MFMA-only source fragments instead.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

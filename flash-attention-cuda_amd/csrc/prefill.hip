@@ -7,38 +7,50 @@
 // scalar FP32 FMAs; here both are dense fp16 contractions on the matrix
 // cores with fp32 accumulation.
 //
+// What bounds this kernel on gfx950 (measured):
+//   * One v_mfma_f32_32x32x16_f16 occupies its SIMD for ~17 ns. VALU work of
+//     OTHER waves on the same SIMD does not run meanwhile; VALU work of the
+//     SAME wave placed between its MFMAs partly does (a few VALU ops, or
+//     ~4 v_exp_f32, per MFMA hide almost completely). The softmax is about as
+//     much VALU time as the two products are MFMA time, so each wave runs a
+//     software pipeline: the MFMAs of its neighbouring tiles interleave with
+//     the softmax of the current one. The second wave on each SIMD covers the
+//     latencies (barrier, LDS reads, loads) of the first.
+//   * LDS serves ~one 64-lane read instruction per 3 ns per CU.
+//
 // Work decomposition
 //   block  = 8 waves, 128 query rows of one (b, h): 4 row waves x 2 key
 //            halves. Row wave r owns rows [32 r, +32); key half h streams the
-//            64-key tiles 2 k + h its rows can see. The two halves keep
-//            separate online-softmax states and merge them through LDS at the
-//            end, so a block's critical path is half its key range.
-//   CU     = one block (128 KiB LDS, <= 256 VGPRs per lane): each SIMD runs
+//            64-key tiles 2 k + h its rows can see. The halves keep separate
+//            online-softmax states and merge them through LDS at the end, so a
+//            block's critical path is half its key range.
+//   CU     = one block (160 KiB LDS, <= 256 VGPRs per lane): each SIMD runs
 //            the two waves of one row wave, one per key half.
 //   grid   = one block per (b, h, 128-row query tile), heaviest (last) query
 //            tiles first: with causal masking the work per block grows with
 //            the query tile, and dispatching in decreasing work order is a
 //            longest-first list schedule over the CUs.
-//   tiles  = K and V stay row-major in LDS (16-byte chunks XOR-swizzled per
-//            row), in one 4-stage ring per key half filled by direct
-//            global->LDS loads (global_load_lds_dwordx4) three of that half's
-//            tiles ahead of the MFMA work.
+//   LDS    = the block's Q tile, plus per key half a 4-stage K ring and a
+//            5-stage V ring of 64-key tiles, all row-major with 16-byte
+//            chunks XOR-swizzled per row, filled by direct global->LDS loads
+//            (global_load_lds_dwordx4) four tiles ahead of use.
 //
-// Main-loop schedule (tiles that need no mask), per wave and step k:
-//   barrier -> issue every LDS fragment read of V and of the next K tile ->
-//   half 0: softmax of S_k, then the burst PV(k) + QK(k+1);
-//   half 1: the burst PV(k) + QK(k+1), then the softmax of S_{k+1}.
-//   The burst interleaves four independent MFMA accumulation chains and runs
-//   at raised wave priority. The two waves that share a SIMD are therefore in
-//   opposite phases: one issues MFMAs while the other runs its exp-heavy
-//   softmax on the VALU. S dies as P is formed, so one S buffer serves both
-//   tiles. Tiles that need a mask (causal diagonal, ragged tail) and query
-//   rows that see fewer than 512 keys take a plain per-tile step.
+// Main loop (tiles that need no mask), per wave and step k of its half:
+//   wait for tile k+2 -> barrier -> issue the loads of tile k+4 ->
+//   O *= alpha_{k-1} (only where a row's max rose) -> row max of S_k ->
+//   { QK(k+1) and PV(k-1) on the matrix cores } interleaved with
+//   { exp / pack / row sum of S_k on the VALU } ->
+//   LDS reads of the next step's fragments (K_{k+2}, V_k), which land while
+//   the next barrier and row max run.
+//   S and P are double-buffered (the loop is unrolled by two), so the MFMAs of
+//   a step never wait for that step's softmax. Tiles that need a mask (causal
+//   diagonal, ragged tail) and query rows that see fewer than 512 keys take a
+//   plain per-tile step.
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
 //                 registers. Each lane ends up with ONE query column and 16 of
-//                 the 32 keys, so a query's softmax state lives in the lane
+//                 each 32 keys, so a query's softmax state lives in the lane
 //                 pair (l, l ^ 32).
 //   O^T += V^T P^T : B = P^T straight from the S^T accumulators (fp32 -> fp16
 //                 pack), A = V^T read with ds_read_b64_tr_b16: inside each
@@ -54,45 +66,41 @@
 // Softmax: log2 domain, p = exp2(s * c - m) with c = |scale| * log2(e) (a
 // negative scale is folded into Q by an exact fp16 negation). m is the exact
 // running max, so the dominant key of a row always enters the PV product as
-// P = 1 exactly; the O rescale is skipped (wave-uniform branch) whenever no
-// row of the wave raised its max. The row sum l is accumulated from the same
-// fp16 P values the PV product consumes (v_dot2_f32_f16), so the weights
-// that multiply V sum to exactly the l they are divided by.
-// On tiles that carry a mask (causal diagonal, ragged tail) and for query
+// P = 1 exactly. The row sum l is accumulated from the same fp16 P values the
+// PV product consumes (v_dot2_f32_f16), so the weights that multiply V sum to
+// exactly the l they are divided by. On tiles that carry a mask and for query
 // rows that see fewer than 512 keys, P is split into hi + lo fp16 parts and
 // the PV product is issued twice: those rows have few, large weights, where
-// one fp16 rounding of P would cost up to ~4e-4 of output accuracy (about
-// 1.6 % extra MFMA work at causal S = 4096).
+// one fp16 rounding of P would cost up to ~4e-4 of output accuracy.
 
 #include "fa_internal.h"
 
 namespace fa {
 namespace {
 
-constexpr int kQWaves = 4;                    // row waves per key half
-constexpr int kThreads = 2 * kQWaves * kWave; // 512: two key halves
+constexpr int kRowWaves = 4;                  // row waves per key half
+constexpr int kWaves = 2 * kRowWaves;         // x 2 key halves
+constexpr int kThreads = kWaves * kWave;      // 512
 constexpr int kRowsPerWave = 32;
-constexpr int kBr = kQWaves * kRowsPerWave;   // 128 query rows per block
+constexpr int kBr = kRowWaves * kRowsPerWave; // 128 query rows per block
 constexpr int kBc = 64;                       // keys per tile
 constexpr int kTileHalves = kBc * kHeadDim;   // 4096 halves = 8 KiB
-constexpr int kStages = 4;
-constexpr int kAhead = kStages - 1;           // tiles in flight ahead of use
+constexpr int kKStages = 4;
+constexpr int kVStages = 5;
+constexpr int kAhead = 4;                     // tiles in flight ahead of use
 constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per tile
 constexpr int kSplitPRowsBelow = 512;  // rows with fewer keys than this: split P
 constexpr float kNegHuge = -3.0e38f;
-// s_waitcnt immediate for vmcnt(0) with expcnt / lgkmcnt left unconstrained.
-constexpr int kWaitVmcnt0 = 0x0F70;
 
-// LDS: [key half][stage][K | V][64 rows x 64 halves] = 128 KiB
-constexpr int kStageHalves = 2 * kTileHalves;
-constexpr int kHalfHalves = kStages * kStageHalves;
-constexpr int kLdsHalves = 2 * kHalfHalves;
+// LDS (halves): [Q: 128 rows x 64] [half 0: K ring | V ring] [half 1: ...]
+constexpr int kQHalves = kBr * kHeadDim;                         // 16 KiB
+constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
+constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 KiB
 
-typedef __attribute__((address_space(3))) void lds_void;
 typedef short short4v __attribute__((ext_vector_type(4)));
 
 // Chunk swizzles (16-byte chunk index within a 128-byte row).
-//  K: a ds_read_b128 phase reads the same logical chunk of 8 (32 banks) or
+//  K, Q: a ds_read_b128 phase reads the same logical chunk of 8 (32 banks) or
 //     16 (64 banks) consecutive rows; f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2)
 //     is a bijection on every 8 consecutive rows and keeps the 8 even and the
 //     8 odd rows of any 16 apart, so both bank layouts are conflict free.
@@ -120,28 +128,6 @@ __device__ __forceinline__ void global_to_lds16(const void *src, const void *lds
       : "memory", "m0");
 }
 
-// Issue the direct global->LDS loads of one 64-key K tile and V tile
-// (256 threads, 4 x 16 B each). Rows past the sequence end are clamped to the
-// last row: they are masked in the softmax (K) and weighted by 0 (V).
-__device__ __forceinline__ void issue_tile_loads(const _Float16 *__restrict__ kp,
-                                                 const _Float16 *__restrict__ vp,
-                                                 _Float16 *stage_lds, int key0,
-                                                 int seq, int tid) {
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int rblock = (w * 2 + it) * 8;  // 8 rows per wave instruction
-    const int r = rblock + (lane >> 3);
-    const int p = lane & 7;
-    const int key = min(key0 + r, seq - 1);
-    const size_t row_off = static_cast<size_t>(key) * kHeadDim;
-    global_to_lds16(kp + row_off + ((p ^ k_swz(r)) << 3), stage_lds + rblock * kHeadDim);
-    global_to_lds16(vp + row_off + ((p ^ v_swz(r)) << 3),
-                    stage_lds + kTileHalves + rblock * kHeadDim);
-  }
-}
-
 // Wait until at most N of this thread's global->LDS loads are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_loads() {
@@ -161,16 +147,21 @@ __device__ __forceinline__ half4 lds_tr16(const _Float16 *p) {
   return __builtin_bit_cast(half4, r);
 }
 
+__device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
+                                         const floatx16 &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 struct SoftmaxState {
   float m;       // running max (log2 domain, already scaled by c)
   float l;       // this lane's share of the row sum
   floatx16 o[2]; // O^T accumulators: d-blocks 0 and 1
 };
 
-// Per-lane LDS offsets (in halves, relative to a stage) of every fragment a
+// Per-lane LDS offsets (in halves, relative to a tile) of every fragment a
 // wave reads from a tile; loop invariant.
 struct FragOffsets {
-  int k[4];  // K fragment for d-step s (32-key block 0; block 1 is +32 rows)
+  int k[4];  // K (and Q) fragment for d-step s (32-key block 0; block 1 is +32 rows)
   int v[2];  // V^T transpose-read base for d-block db (key sub-blocks add rows)
 };
 
@@ -188,7 +179,7 @@ __device__ __forceinline__ FragOffsets frag_offsets(int lane) {
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
     const int d = db * 32 + tr_dim;
-    f.v[db] = kTileHalves + tr_row * kHeadDim + (((d >> 3) ^ v_swz(tr_row)) << 3) + (d & 7);
+    f.v[db] = tr_row * kHeadDim + (((d >> 3) ^ v_swz(tr_row)) << 3) + (d & 7);
   }
   return f;
 }
@@ -197,25 +188,43 @@ __device__ __forceinline__ FragOffsets frag_offsets(int lane) {
 struct KFrags { half8 f[2][4]; };  // [32-key block][d-step]
 struct VFrags { half8 f[4][2]; };  // [16-key step][d-block]
 
+typedef __attribute__((address_space(3))) const _Float16 lds_half;
+
+// An LDS address the compiler must materialise as one register per step:
+// the constant row offsets of the reads below then fold into the
+// instructions' offset fields instead of being hoisted out of the loop as
+// separate loop-invariant addresses.
+__device__ __forceinline__ lds_half *opaque_lds(const _Float16 *p) {
+  unsigned a = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p)));
+  asm volatile("" : "+v"(a));
+  return reinterpret_cast<lds_half *>(static_cast<uintptr_t>(a));
+}
+
 __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
                                        const FragOffsets &fo, KFrags &k) {
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int s = 0; s < 4; ++s) {
+    lds_half *p = opaque_lds(tile + fo.k[s]);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) k.f[kb][s] = lds_b128(tile + fo.k[s] + kb * 32 * kHeadDim);
+    for (int kb = 0; kb < 2; ++kb)
+      k.f[kb][s] = *reinterpret_cast<__attribute__((address_space(3))) const half8 *>(
+          p + kb * 32 * kHeadDim);
+  }
 }
 
 __device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
                                        const FragOffsets &fo, VFrags &v) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int kb = ks >> 1, h = ks & 1;
+  for (int db = 0; db < 2; ++db) {
+    lds_half *p = opaque_lds(tile + fo.v[db]);
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kb = ks >> 1, h = ks & 1;
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
-        const int row_off = (kb * 32 + 16 * h + 8 * part) * kHeadDim;
-        const half4 v4 = lds_tr16(tile + fo.v[db] + row_off);
+        const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) short4v *)(p + (kb * 32 + 16 * h + 8 * part) * kHeadDim));
+        const half4 v4 = __builtin_bit_cast(half4, r);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v.f[ks][db][4 * part + e] = v4[e];
       }
@@ -223,9 +232,26 @@ __device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
   }
 }
 
-__device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
-                                         const floatx16 &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+// S^T[kb] = K_kb Q^T for both 32-key blocks (8 MFMAs, two chains).
+__device__ __forceinline__ void qk_mfma(const KFrags &k, const half8 (&qf)[4],
+                                        floatx16 (&s)[2]) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
+}
+
+// O^T[db] += V^T_db P^T (8 MFMAs, two chains).
+__device__ __forceinline__ void pv_mfma(const VFrags &v, const half8 (&p)[4],
+                                        floatx16 (&o)[2]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) o[db] = mfma(v.f[ks][db], p[ks], o[db]);
 }
 
 // max(x[l], x[l ^ 32]) for every lane: one v_permlane32_swap (VALU), no LDS.
@@ -245,54 +271,49 @@ __device__ __forceinline__ float max_lane_pair(float x) {
   return a;
 }
 
-// Online softmax of one S^T tile, producing P^T fragments (hi [+ lo]).
-// MASK: keys past the end or above the causal diagonal;
-// SPLIT: P feeds the PV product as hi + lo fp16 parts.
-template <bool CAUSAL, bool MASK, bool SPLIT>
-__device__ __forceinline__ void softmax_tile(floatx16 (&s_acc)[2], int key0, int seq,
-                                             int my_q, int lane, float c_scale,
-                                             SoftmaxState &st, half8 (&p_hi)[4],
-                                             half8 (&p_lo)[4]) {
-  // Element a of key block kb holds key key0 + kb*32 + 8 (a/4) + 4 g + a%4;
-  // it is visible iff that offset is <= lim (last visible key - key0 - 4 g).
-  const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
+// New running max for one tile; returns alpha, the factor that rescales the
+// previous O and l (l is rescaled here, O by the caller).
+// MASK: keys past the end or above the causal diagonal become -inf.
+template <bool CAUSAL, bool MASK>
+__device__ __forceinline__ float tile_max(floatx16 (&s)[2], int lim, float c_scale,
+                                          SoftmaxState &st) {
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       if (MASK)
-        s_acc[kb][a] = (kb * 32 + 8 * (a >> 2) + (a & 3) <= lim) ? s_acc[kb][a] : -INFINITY;
-      mx = fmaxf(mx, s_acc[kb][a]);
+        s[kb][a] = (kb * 32 + 8 * (a >> 2) + (a & 3) <= lim) ? s[kb][a] : -INFINITY;
+      mx = fmaxf(mx, s[kb][a]);
     }
   }
   mx = max_lane_pair(mx);
-  const float mx_scaled = mx * c_scale;
-  const bool raise = mx_scaled > st.m;
-  if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-    const float m_new = raise ? mx_scaled : st.m;
-    const float alpha = fast_exp2(st.m - m_new);
-    st.m = m_new;
-    st.l *= alpha;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) st.o[db][a] *= alpha;
-  }
-  const float m_use = st.m;
+  const float m_new = fmaxf(st.m, mx * c_scale);
+  const float alpha = fast_exp2(st.m - m_new);
+  st.m = m_new;
+  st.l *= alpha;
+  return alpha;
+}
 
+// P^T fragments (hi [+ lo]) of one tile and the row-sum update.
+template <bool MASK, bool SPLIT>
+__device__ __forceinline__ void tile_exp(const floatx16 (&s)[2], float c_scale,
+                                         SoftmaxState &st, half8 (&p_hi)[4],
+                                         half8 (&p_lo)[4]) {
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  const float m_use = st.m;
   float lsum = 0.f;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int kb = ks >> 1, h = ks & 1;
 #pragma unroll
     for (int t = 0; t < 8; t += 2) {
-      float p0 = fast_exp2(fmaf(s_acc[kb][8 * h + t], c_scale, -m_use));
-      float p1 = fast_exp2(fmaf(s_acc[kb][8 * h + t + 1], c_scale, -m_use));
+      const float s0 = s[kb][8 * h + t], s1 = s[kb][8 * h + t + 1];
+      float p0 = fast_exp2(fmaf(s0, c_scale, -m_use));
+      float p1 = fast_exp2(fmaf(s1, c_scale, -m_use));
       if (MASK) {
-        p0 = (s_acc[kb][8 * h + t] == -INFINITY) ? 0.f : p0;
-        p1 = (s_acc[kb][8 * h + t + 1] == -INFINITY) ? 0.f : p1;
+        p0 = (s0 == -INFINITY) ? 0.f : p0;
+        p1 = (s1 == -INFINITY) ? 0.f : p1;
       }
       const half2 hi2 = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
       p_hi[ks][t] = hi2[0];
@@ -310,80 +331,100 @@ __device__ __forceinline__ void softmax_tile(floatx16 (&s_acc)[2], int key0, int
   st.l += lsum;
 }
 
-// PV(t) and QK(t+1) as four independent accumulation chains (O d-blocks 0/1,
-// S key-blocks 0/1), issued alternately.
-template <bool WITH_QK>
-__device__ __forceinline__ void pv_qk_mfma(const VFrags &v, const half8 (&p)[4],
-                                           const KFrags &k, const half8 (&qf)[4],
-                                           floatx16 (&o)[2], floatx16 (&s)[2]) {
-  if (WITH_QK) {
+// O *= alpha when the max of any row of the wave rose (wave-uniform branch;
+// alpha is exactly 1 otherwise).
+__device__ __forceinline__ void rescale_o(SoftmaxState &st, float alpha) {
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
+      for (int a = 0; a < 16; ++a) st.o[db][a] *= alpha;
   }
+}
+
+// Scheduling pipeline for one main step: each of its 16 MFMAs followed by a
+// group of VALU instructions (the softmax of the other tile), then a hard
+// scheduling boundary so no compute sinks below the next step's barrier.
+__device__ __forceinline__ void interleave_step() {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      o[db] = mfma(v.f[i][db], p[i], o[db]);
-      if (WITH_QK) s[db] = mfma(k.f[db][i], qf[i], s[db]);
-    }
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
   }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Pins the P fragments of a step to that step: without a use there, the
+// compiler sinks their computation into the next step (next to the PV MFMAs
+// that consume them), which defeats the interleave.
+__device__ __forceinline__ void keep(const half8 (&p)[4]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(p[ks]));
 }
 
 // Plain (non-pipelined) step for masked / short-row tiles: QK, softmax with
 // mask and split P, PV issued twice.
 template <bool CAUSAL>
-__device__ __forceinline__ void slow_step(const _Float16 *__restrict__ tile,
-                                          const FragOffsets &fo, const half8 (&qf)[4],
-                                          int key0, int seq, int my_q, int lane,
-                                          float c_scale, SoftmaxState &st) {
-  KFrags k;
-  VFrags v;
-  read_k(tile, fo, k);
-  read_v(tile, fo, v);
+__device__ __forceinline__ void slow_step(const KFrags &kf, const VFrags &vf,
+                                          const half8 (&qf)[4], int key0, int seq,
+                                          int my_q, int lane, float c_scale,
+                                          SoftmaxState &st) {
   floatx16 s[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-    for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
-  }
+  qk_mfma(kf, qf, s);
+  // Element a of key block kb holds key key0 + kb*32 + 8 (a/4) + 4 g + a%4;
+  // it is visible iff that offset is <= lim (last visible key - key0 - 4 g).
+  const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
+  const float alpha = tile_max<CAUSAL, true>(s, lim, c_scale, st);
+  rescale_o(st, alpha);
   half8 p_hi[4], p_lo[4];
-  softmax_tile<CAUSAL, true, true>(s, key0, seq, my_q, lane, c_scale, st, p_hi, p_lo);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      st.o[db] = mfma(v.f[i][db], p_hi[i], st.o[db]);
-      st.o[db] = mfma(v.f[i][db], p_lo[i], st.o[db]);
-    }
-  }
+  tile_exp<true, true>(s, c_scale, st, p_hi, p_lo);
+  pv_mfma(vf, p_hi, st.o);
+  pv_mfma(vf, p_lo, st.o);
 }
 
-// Tile ring of one key half: half h owns tiles 2k + h (k = 0, 1, ...), stage
-// k % kStages of its LDS region.
+// The K and V rings of one key half: half h owns tiles 2 k + h (k = 0, 1,
+// ...), in K stage k % kKStages and V stage k % kVStages.
 struct HalfRing {
-  _Float16 *lds;
+  _Float16 *kring, *vring;
   const _Float16 *kp, *vp;
-  int seq, n_tiles, half, htid;
+  int seq, n_tiles, half;
+  int src_off[2][2];  // [K|V][row block i]: this lane's chunk within its row
+  int row_in_tile[2];
+  int lds_off[2];     // row block i of this wave, in halves
 
   __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
-  __device__ __forceinline__ _Float16 *stage(int k) const {
-    return lds + (k & (kStages - 1)) * kStageHalves;
+  __device__ __forceinline__ bool exists(int k) const { return tile(k) < n_tiles; }
+  __device__ __forceinline__ _Float16 *kstage(int k) const {
+    return kring + (k % kKStages) * kTileHalves;
   }
+  __device__ __forceinline__ _Float16 *vstage(int k) const {
+    return vring + (k % kVStages) * kTileHalves;
+  }
+  // The half's four waves each load row blocks {2 wh, 2 wh + 1} (8 rows of
+  // 128 B each) of K and of V; lane = 8 * (row in block) + chunk. Rows past
+  // the sequence end are clamped to the last row: they are masked in the
+  // softmax (K) and weighted by 0 (V).
   __device__ __forceinline__ void issue(int k) const {
-    if (tile(k) < n_tiles) issue_tile_loads(kp, vp, stage(k), tile(k) * kBc, seq, htid);
+    if (!exists(k)) return;
+    const int key0 = tile(k) * kBc;
+    _Float16 *const ks = kstage(k);
+    _Float16 *const vs = vstage(k);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * kHeadDim;
+      global_to_lds16(kp + row + src_off[0][i], ks + lds_off[i]);
+      global_to_lds16(vp + row + src_off[1][i], vs + lds_off[i]);
+    }
   }
-  // Start of step k: this half's tiles k and k+1 are resident and visible to
-  // the whole block, then the load of its tile k + kAhead is issued into the
-  // stage tile k-1 used (every wave finished reading it before the barrier).
+  // Start of main step k: this half's tiles up to k + 2 are resident and
+  // visible to the whole block, then the loads of tile k + 4 are issued.
+  // Its K stage last held tile k, its V stage tile k - 1: the main loop read
+  // them at the end of steps k - 2 and k - 1, the masked step reads a tile
+  // before its own barrier.
   // A plain s_barrier: __syncthreads() would add a release fence, which
   // drains every outstanding load of the ring.
   __device__ __forceinline__ void advance(int k) const {
-    if (tile(k + 2) < n_tiles)
+    if (exists(k + 3))
       wait_loads<kLoadsPerTile>();
     else
       wait_loads<0>();
@@ -407,26 +448,41 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int rw = wave & (kQWaves - 1);  // row wave: rows [32 rw, +32)
-  const int half = wave / kQWaves;      // key half: tiles 2k + half
-  const int htid = tid & (kQWaves * kWave - 1);
+  // Wave-uniform (SGPR) so every stage / row-block address below is scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rw = wave & (kRowWaves - 1);  // row wave: rows [32 rw, +32)
+  const int half = wave / kRowWaves;      // key half: tiles 2k + half
   const int col = lane & 31;
-  const int g = lane >> 5;
 
   const size_t head_off = static_cast<size_t>(bh) * seq * kHeadDim;
-  const _Float16 *qp = q + head_off;
-
   const int q0 = qtile * kBr;
   const int qw0 = q0 + rw * kRowsPerWave;
   const int my_q = qw0 + col;
 
   const int key_end = CAUSAL ? min(seq, q0 + kBr) : seq;
   const int n_tiles = (key_end + kBc - 1) / kBc;
-  HalfRing ring{lds + half * kHalfHalves, k + head_off, v + head_off, seq, n_tiles,
-                half, htid};
+  _Float16 *const half_lds = lds + kQHalves + half * kHalfHalves;
+  _Float16 *const q_lds = lds;
+  HalfRing ring;
+  ring.kring = half_lds;
+  ring.vring = half_lds + kKStages * kTileHalves;
+  ring.kp = k + head_off;
+  ring.vp = v + head_off;
+  ring.seq = seq;
+  ring.n_tiles = n_tiles;
+  ring.half = half;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rblock = 2 * rw + i;
+    const int r = rblock * 8 + (lane >> 3);
+    const int p = lane & 7;
+    ring.row_in_tile[i] = r;
+    ring.src_off[0][i] = (p ^ k_swz(r)) << 3;
+    ring.src_off[1][i] = (p ^ v_swz(r)) << 3;
+    ring.lds_off[i] = rblock * 8 * kHeadDim;
+  }
   const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
-  // Tiles [0, 2 n_main) need no mask for any wave of the block and all its
+  // Tiles [0, 2 n_main) need no mask for any row of the block, and all its
   // rows see >= kSplitPRowsBelow keys: each half runs n_main pipelined steps
   // on them. The rest (causal diagonal, ragged tail, short rows) take the
   // plain masked step.
@@ -435,29 +491,31 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
 
+  // Q tile (16 row blocks of 8 rows, 2 per wave; K swizzle), then this
+  // half's first kAhead tiles.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rblock = 2 * wave + i;
+    const int r = rblock * 8 + (lane >> 3);
+    const int row = min(q0 + r, seq - 1);
+    global_to_lds16(q + head_off + static_cast<size_t>(row) * kHeadDim +
+                        (((lane & 7) ^ k_swz(r)) << 3),
+                    q_lds + rblock * 8 * kHeadDim);
+  }
 #pragma unroll
   for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
+  wait_loads<0>();
+  __builtin_amdgcn_s_barrier();
 
+  const FragOffsets fo = frag_offsets(lane);
   // Q^T fragments: lane holds query my_q, head dims [32 g + 8 s, +8).
   half8 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    if (my_q < seq) {
-      qf[s] = *reinterpret_cast<const half8 *>(
-          qp + static_cast<size_t>(my_q) * kHeadDim + 32 * g + 8 * s);
-      if (negate_q) qf[s] = -qf[s];
-    } else {
-      qf[s] = half8{};
-    }
+    qf[s] = lds_b128(q_lds + rw * kRowsPerWave * kHeadDim + fo.k[s]);
+    if (negate_q) qf[s] = -qf[s];
   }
-  // One wait the compiler can see (it cannot see the ring's asm waits): Q and
-  // the first kAhead tiles are resident, and no compiler-issued load is
-  // pending inside the loops, so it adds no vmcnt waits there.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __builtin_amdgcn_s_barrier();
-  ring.issue(kAhead);
 
-  const FragOffsets fo = frag_offsets(lane);
   SoftmaxState st;
   st.m = kNegHuge;
   st.l = 0.f;
@@ -466,61 +524,96 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 #pragma unroll
     for (int a = 0; a < 16; ++a) st.o[db][a] = 0.f;
 
-  // ---- pipelined main loop, ping-pong between the halves --------------------
-  // Step kk, half 0: softmax S(kk) -> burst [PV(kk), QK(kk+1)].
-  //          half 1: burst [PV(kk), QK(kk+1)] -> softmax S(kk+1).
-  // The two waves sharing a SIMD (same row wave, different half) are thus in
-  // opposite phases: one issues MFMAs while the other runs the exp-heavy
-  // softmax. The burst runs at raised priority so its MFMAs issue first.
-  floatx16 s_acc[2];
-  KFrags kf;
-  VFrags vf;
-  half8 p_hi[4], p_lo[4];
-  if (n_main > 0) {
-    read_k(ring.stage(0), fo, kf);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int a = 0; a < 16; ++a) s_acc[kb][a] = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s_acc[kb] = mfma(kf.f[kb][i], qf[i], s_acc[kb]);
-    }
-    if (half == 1)
-      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(0) * kBc, seq, my_q, lane,
-                                         c_scale, st, p_hi, p_lo);
-  }
+  // ---- pipelined main loop ---------------------------------------------------
+  // Step k: MFMAs QK(k+1) [K_{k+1}, read at step k-1] and PV(k-1) [P_{k-1},
+  // V_{k-1}] interleave with the softmax of S_k. S, P and the K fragments
+  // alternate between even and odd steps. QK(k+1) is issued unconditionally:
+  // on the last main step it reads whatever K stage k+1 holds (in bounds)
+  // and the result is discarded.
   int kk = 0;
-  for (; kk < n_main; ++kk) {
-    if (kk > 0) ring.advance(kk);
-    // QK(kk+1) is issued unconditionally: on the last main step it reads
-    // whatever stage kk+1 holds (in bounds) and the result is discarded,
-    // which keeps the accumulators in place (a branch makes the compiler
-    // copy them every step).
-    read_v(ring.stage(kk), fo, vf);
-    read_k(ring.stage(kk + 1), fo, kf);
-    if (half == 0)
-      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(kk) * kBc, seq, my_q,
-                                         lane, c_scale, st, p_hi, p_lo);
-    __builtin_amdgcn_s_setprio(2);
-    pv_qk_mfma<true>(vf, p_hi, kf, qf, st.o, s_acc);
-    __builtin_amdgcn_s_setprio(0);
-    if (half == 1 && kk + 1 < n_main)
-      softmax_tile<CAUSAL, false, false>(s_acc, ring.tile(kk + 1) * kBc, seq, my_q,
-                                         lane, c_scale, st, p_hi, p_lo);
+  if (n_main > 0) {
+    floatx16 s_a[2], s_b[2];
+    half8 p_a[4], p_b[4], p_unused[4];
+    KFrags kf;
+    VFrags vf;
+    float alpha;
+    read_k(ring.kstage(0), fo, kf);
+    qk_mfma(kf, qf, s_a);
+    read_k(ring.kstage(1), fo, kf);
+
+    // step 0 (no PV yet)
+    ring.advance(0);
+    alpha = tile_max<CAUSAL, false>(s_a, 0, c_scale, st);
+    qk_mfma(kf, qf, s_b);
+    tile_exp<false, false>(s_a, c_scale, st, p_a, p_unused);
+    __builtin_amdgcn_sched_barrier(0);
+    read_k(ring.kstage(2), fo, kf);
+    read_v(ring.vstage(0), fo, vf);
+    kk = 1;
+
+    // steps kk (odd: S_kk in s_b, P_{kk-1} in p_a) and kk + 1 (even); kf and
+    // vf hold K_{kk+1} and V_{kk-1}
+    for (; kk + 1 < n_main; kk += 2) {
+      ring.advance(kk);
+      rescale_o(st, alpha);
+      alpha = tile_max<CAUSAL, false>(s_b, 0, c_scale, st);
+      qk_mfma(kf, qf, s_a);
+      pv_mfma(vf, p_a, st.o);
+      tile_exp<false, false>(s_b, c_scale, st, p_b, p_unused);
+      interleave_step();
+      keep(p_b);
+      read_k(ring.kstage(kk + 2), fo, kf);
+      read_v(ring.vstage(kk), fo, vf);
+
+      ring.advance(kk + 1);
+      rescale_o(st, alpha);
+      alpha = tile_max<CAUSAL, false>(s_a, 0, c_scale, st);
+      qk_mfma(kf, qf, s_b);
+      pv_mfma(vf, p_b, st.o);
+      tile_exp<false, false>(s_a, c_scale, st, p_a, p_unused);
+      interleave_step();
+      keep(p_a);
+      read_k(ring.kstage(kk + 3), fo, kf);
+      read_v(ring.vstage(kk + 1), fo, vf);
+    }
+    // Here step kk - 1 is done: S_kk in s_b, P_{kk-1} in p_a, V_{kk-1} in vf.
+    if (kk < n_main) {  // one more (odd) step: no QK beyond the main tiles
+      ring.advance(kk);
+      rescale_o(st, alpha);
+      alpha = tile_max<CAUSAL, false>(s_b, 0, c_scale, st);
+      pv_mfma(vf, p_a, st.o);
+      tile_exp<false, false>(s_b, c_scale, st, p_b, p_unused);
+      read_v(ring.vstage(kk), fo, vf);
+      rescale_o(st, alpha);
+      pv_mfma(vf, p_b, st.o);
+      ++kk;
+    } else {
+      rescale_o(st, alpha);
+      pv_mfma(vf, p_a, st.o);
+    }
   }
 
   // ---- masked / short-row tiles: one plain step per tile ---------------------
+  // Tile kk is resident (waited for by an earlier advance, or by the
+  // prologue); its fragments are read before the barrier that lets the load
+  // of tile kk + 4 overwrite its K stage.
   for (; kk < n_steps; ++kk) {
-    if (kk > 0) ring.advance(kk);
     const int key0 = ring.tile(kk) * kBc;
-    if (key0 < wave_key_end)
-      slow_step<CAUSAL>(ring.stage(kk), fo, qf, key0, seq, my_q, lane, c_scale, st);
+    const bool active = key0 < wave_key_end;
+    KFrags kf;
+    VFrags vf;
+    if (active) {
+      read_k(ring.kstage(kk), fo, kf);
+      read_v(ring.vstage(kk), fo, vf);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done
+    ring.advance(kk);
+    if (active) slow_step<CAUSAL>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
   }
 
   // ---- merge the two halves through LDS, normalise, store ------------------
-  // Layout: [row wave][34 values][64 lanes] fp32, reusing the tile buffers.
-  // Every load the ring issued has completed (the last steps waited with
-  // vmcnt(0)); the barrier ends every read of the tiles.
+  // Layout: [row wave][34 values][64 lanes] fp32 from the start of LDS. Every
+  // load the ring issued has completed; the barrier ends every read of it.
   wait_loads<0>();
   __builtin_amdgcn_s_barrier();
   float *xchg = reinterpret_cast<float *>(lds) + rw * (34 * kWave) + lane;
@@ -549,6 +642,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }
 
   // ---- epilogue: O = O^T / l, one query row per lane -------------------------
+  const int g = lane >> 5;
   const float l_tot = st.l + __shfl_xor(st.l, 32);
   const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
   if (my_q < seq) {
