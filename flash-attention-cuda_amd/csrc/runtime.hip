@@ -111,7 +111,12 @@ int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks) {
   return FA_DECODE_SPLIT_MIN;
 }
 
-// csrc/decode.cu:205-206: two blocks per compute unit.
+// csrc/decode.cu:205-206 sets two split blocks per SM. Here a split-K unit is
+// one wave, and the unit count the chooser aims for is 16 per compute unit
+// (four per SIMD): enough units that the dispatcher keeps every SIMD busy
+// and evens out ragged sequence lengths.
+constexpr int kDecodeUnitsPerCu = 16;
+
 int fa_decode_min_blocks(int device, int *min_blocks) {
   clear_error();
   if (min_blocks == nullptr)
@@ -120,7 +125,7 @@ int fa_decode_min_blocks(int device, int *min_blocks) {
   if (cu <= 0)
     return set_error(FA_ERR_HIP, "could not query the compute-unit count of device %d",
                      device);
-  *min_blocks = 2 * cu;
+  *min_blocks = kDecodeUnitsPerCu * cu;
   return FA_OK;
 }
 
