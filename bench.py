@@ -323,7 +323,7 @@ def main():
             "sum_len": d["sum_len"],
             "bytes_per_step": d["bytes"],
             "cache_copies_rotated": d["copies"],
-            "roofline": {"bound": "hbm", "kernel": "decode_split_kernel + decode_merge_kernel",
+            "roofline": {"bound": "hbm", "kernel": "decode_bh_kernel",
                          "achieved": gbs_kern, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs_kern / HBM_PEAK_GBS, "kernel_ms": d["kernel_ms"],
                          "traffic": load_traffic("decode_c5_traffic.txt")},

@@ -2,10 +2,18 @@
 //
 // Reference behaviour: csrc/decode.cu:50-240 of shrvan30/flash-attention-cuda
 // (split pass :50-138, log-sum-exp merge :143-175, chunk chooser :183-192,
-// launcher :194-240). The work split is the same (the cache rows of each
-// (batch, head) are cut into chunks of `chunk` rows, each chunk yields a
-// partial (m, l, acc[64]), then a merge); everything below the work split is
-// laid out for CDNA4 instead:
+// launcher :194-240). The result is the same softmax(q K^T * scale) V over the
+// first seq_lens[b] cache rows; the work split depends on the grid:
+//
+//  * B * H < compute units (too few (b, h) pairs to fill the chip): the
+//    reference's split-K scheme. The cache rows of each (b, h) are cut into
+//    chunks of `chunk` rows, each chunk yields a partial (m, l, acc[64]) in
+//    the workspace, and a merge kernel combines them.
+//  * B * H >= compute units: one 8-wave block per (b, h) folds the whole
+//    sequence (decode_bh_kernel below), merging its waves through LDS, so no
+//    partials reach HBM and there is no second kernel.
+//
+// Split path details, laid out for CDNA4:
 //
 //  * One WAVE owns one (b, h, chunk) unit; a block is four independent waves
 //    (no LDS, no barrier). Chunks past a sequence's end exit at once.
@@ -27,6 +35,8 @@
 // produces and consumes them.
 
 #include <hip/hip_fp16.h>
+
+#include <mutex>
 
 #include "fa_internal.h"
 
@@ -51,16 +61,19 @@ __device__ __forceinline__ uint4 load_stream(const _Float16 *p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
-struct RowSlots {
-  uint4 k[kGroupsPerStep];
-  uint4 v[kGroupsPerStep];
+template <int G>
+struct RowSlotsT {
+  uint4 k[G];
+  uint4 v[G];
 };
+typedef RowSlotsT<kGroupsPerStep> RowSlots;
 
-__device__ __forceinline__ void load_slots(RowSlots &r, const _Float16 *kp,
+template <int G>
+__device__ __forceinline__ void load_slots(RowSlotsT<G> &r, const _Float16 *kp,
                                            const _Float16 *vp, int row0,
                                            int end, int sub, int slice) {
 #pragma unroll
-  for (int u = 0; u < kGroupsPerStep; ++u) {
+  for (int u = 0; u < G; ++u) {
     const int row = row0 + u * kRowsPerGroup + sub;
     if (row < end) {
       const size_t off = static_cast<size_t>(row) * kHeadDim + slice * 8;
@@ -83,13 +96,14 @@ __device__ __forceinline__ void unpack8(const uint4 &raw, float f[8]) {
 }
 
 // Fold one sub-step of rows (already loaded) into the running state.
-__device__ __forceinline__ void consume_slots(const RowSlots &r,
+template <int G>
+__device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r,
                                               const float qf[8], int row0,
                                               int end, int sub, float &m,
                                               float &l, float acc[8]) {
-  float s[kGroupsPerStep];
+  float s[G];
 #pragma unroll
-  for (int u = 0; u < kGroupsPerStep; ++u) {
+  for (int u = 0; u < G; ++u) {
     float kf[8];
     unpack8(r.k[u], kf);
     float part = 0.f;
@@ -101,13 +115,13 @@ __device__ __forceinline__ void consume_slots(const RowSlots &r,
   }
   float mx = s[0];
 #pragma unroll
-  for (int u = 1; u < kGroupsPerStep; ++u) mx = fmaxf(mx, s[u]);
+  for (int u = 1; u < G; ++u) mx = fmaxf(mx, s[u]);
   const float m_new = fmaxf(m, mx);
   const float alpha = fast_exp2(m - m_new);
-  float p[kGroupsPerStep];
+  float p[G];
   float psum = 0.f;
 #pragma unroll
-  for (int u = 0; u < kGroupsPerStep; ++u) {
+  for (int u = 0; u < G; ++u) {
     p[u] = fast_exp2(s[u] - m_new);  // masked rows: exp2(-inf) = 0
     psum += p[u];
   }
@@ -115,7 +129,7 @@ __device__ __forceinline__ void consume_slots(const RowSlots &r,
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
-  for (int u = 0; u < kGroupsPerStep; ++u) {
+  for (int u = 0; u < G; ++u) {
     float vf[8];
     unpack8(r.v[u], vf);
 #pragma unroll
@@ -303,14 +317,228 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   }
 }
 
+// Whole-sequence variant for batches with at least one (b, h) per compute
+// unit: one block of 8 waves owns one (b, h), and wave w folds the chunks
+// w, w + 8, w + 16, ... of `chunk` rows each. Rows go in sub-steps of 32, the
+// next one in flight while the current one is consumed; the 8 wave states
+// merge through LDS and the block writes the output, so there is no partial
+// workspace and no merge pass.
+// With chunk == 0 (the automatic choice) the chunk follows the grid:
+//  * every block resident at once (target_waves > 0): the batch's cache rows
+//    over target_waves, so about target_waves waves stream rows, each a long
+//    contiguous range (measured on ragged batches: fewer, longer streams beat
+//    more, shorter ones);
+//  * more blocks than fit (target_waves == 0): 1/8 of the block's own
+//    sequence, so all 8 waves of each resident block stream.
+// Chunks are multiples of 64 rows. Blocks take the sequences in decreasing
+// length order (every block ranks the batch's lengths itself, for batches of
+// up to kRankMax), so the dispatcher runs a longest-first list schedule.
+constexpr int kBhWaves = 8;
+constexpr int kBhThreads = kBhWaves * kWave;
+constexpr int kBhGroups = 4;  // 32-row sub-steps
+constexpr int kRankMax = 256;   // ranking costs batch^2 / 512 LDS reads per thread
+constexpr int kBhWavesPerCu = 5;  // streaming waves per CU when the grid is resident
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
+    const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
+    const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
+    void *__restrict__ o, int batch, int heads, int max_seq, int chunk,
+    int target_waves, float qscale) {
+  __shared__ int s_len[kRankMax];
+  __shared__ int s_order[kRankMax];
+  __shared__ float s_acc[kBhWaves][kHeadDim];
+  __shared__ float s_m[kBhWaves];
+  __shared__ float s_l[kBhWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  int b = static_cast<int>(blockIdx.x) / heads;
+  const int h = static_cast<int>(blockIdx.x) % heads;
+  if (batch <= kRankMax) {
+    // rank(t) = #{u : len_u > len_t or (len_u == len_t and u < t)}: block i
+    // takes the (i / H)-th longest sequence.
+    for (int t = tid; t < batch; t += kBhThreads) s_len[t] = max(0, min(seq_lens[t], max_seq));
+    __syncthreads();
+    for (int t = tid; t < batch; t += kBhThreads) {
+      const int lt = s_len[t];
+      int rank = 0;
+      for (int u = 0; u < batch; ++u) {
+        const int lu = s_len[u];
+        rank += (lu > lt || (lu == lt && u < t)) ? 1 : 0;
+      }
+      s_order[rank] = t;
+    }
+    __syncthreads();
+    b = s_order[b];
+  }
+  const int bh = b * heads + h;
+  const int len = max(0, min(seq_lens[b], max_seq));
+  if (chunk == 0) {
+    int rows_per_wave;
+    if (target_waves > 0) {
+      int part = 0;
+      for (int t = lane; t < batch; t += kWave)
+        part += batch <= kRankMax ? s_len[t] : max(0, min(seq_lens[t], max_seq));
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+      const float total = static_cast<float>(__builtin_amdgcn_readfirstlane(part));
+      rows_per_wave = static_cast<int>(
+          fminf(ceilf(total * static_cast<float>(heads) / static_cast<float>(target_waves)),
+                static_cast<float>(max_seq)));
+    } else {
+      rows_per_wave = (len + kBhWaves - 1) / kBhWaves;
+    }
+    chunk = max(64, (rows_per_wave + 63) & ~63);
+  }
+  chunk = min(chunk, max_seq);  // max_seq <= 2^27 (host check): 8 * chunk fits in int
+
+  const int sub = lane >> 3;   // row inside an 8-row group
+  const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const _Float16 *kp = k_cache + head_off;
+  const _Float16 *vp = v_cache + head_off;
+
+  float m = kNegBig, l = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+
+  constexpr int kStepRows = kRowsPerGroup * kBhGroups;  // 32
+  const int stride = kBhWaves * chunk;  // distance between a wave's chunks
+  int c0 = wave * chunk;                // this wave's current chunk
+  if (c0 < len) {
+    float qf[8];
+    {
+      const uint4 raw = *reinterpret_cast<const uint4 *>(
+          q + static_cast<size_t>(bh) * kHeadDim + slice * 8);
+      unpack8(raw, qf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[e] *= qscale;
+    }
+    int end = min(len, c0 + chunk);
+    int row0 = c0;
+    RowSlotsT<kBhGroups> cur, nxt;
+    load_slots(cur, kp, vp, row0, end, sub, slice);
+    for (;;) {
+      // Next sub-step: the rest of this chunk, else this wave's next chunk.
+      int n_row0 = row0 + kStepRows, n_end = end, n_c0 = c0;
+      if (n_row0 >= end) {
+        n_c0 = c0 + stride;
+        n_row0 = n_c0;
+        n_end = min(len, n_c0 + chunk);
+      }
+      const bool more = n_row0 < n_end;
+      if (more) load_slots(nxt, kp, vp, n_row0, n_end, sub, slice);
+      consume_slots(cur, qf, row0, end, sub, m, l, acc);
+      if (!more) break;
+      cur = nxt;
+      row0 = n_row0;
+      end = n_end;
+      c0 = n_c0;
+    }
+  }
+
+  // Merge the 8 row groups of the wave (lanes that share `slice`).
+#pragma unroll
+  for (int off = 8; off < kWave; off <<= 1) {
+    const float mb = __shfl_xor(m, off);
+    const float lb = __shfl_xor(l, off);
+    float accb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[e], off);
+    merge_state(m, l, acc, mb, lb, accb);
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_acc[wave][slice * 8 + e] = acc[e];
+    if (slice == 0) {
+      s_m[wave] = m;
+      s_l[wave] = l;
+    }
+  }
+  __syncthreads();
+  if (tid < kHeadDim) {
+    float mb = s_m[0];
+#pragma unroll
+    for (int w = 1; w < kBhWaves; ++w) mb = fmaxf(mb, s_m[w]);
+    float lb = 0.f, ab = 0.f;
+#pragma unroll
+    for (int w = 0; w < kBhWaves; ++w) {
+      const float f = fast_exp2(s_m[w] - mb);  // empty waves: l = 0, acc = 0
+      lb = fmaf(s_l[w], f, lb);
+      ab = fmaf(s_acc[w][tid], f, ab);
+    }
+    // decode.cu:172: a sequence with no rows gets a zero output.
+    const float out = (lb > 0.f) ? ab / lb : 0.f;
+    const size_t idx = static_cast<size_t>(bh) * kHeadDim + tid;
+    if (OUT_F32)
+      static_cast<float *>(o)[idx] = out;
+    else
+      static_cast<_Float16 *>(o)[idx] = static_cast<_Float16>(out);
+  }
+}
+
 }  // namespace
+
+// Blocks of decode_bh_kernel resident on one CU at once, per device.
+int bh_blocks_per_cu(int device) {
+  static std::once_flag once[kMaxDevices];
+  static int blocks[kMaxDevices];
+  if (device < 0 || device >= kMaxDevices) return 1;
+  std::call_once(once[device], [device] {
+    int n = 0;
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    if (hipSetDevice(device) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void *>(decode_bh_kernel<false>), kBhThreads, 0) !=
+            hipSuccess)
+      n = 0;
+    hipSetDevice(prev);
+    blocks[device] = n;
+  });
+  return blocks[device] > 0 ? blocks[device] : 1;
+}
+
+// Whole-sequence blocks need at least one (b, h) per compute unit to fill
+// the chip; below that, the split-K grid spreads each sequence over CUs.
+bool use_bh_path(int batch, int heads) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const int cu = device_cu_count(dev);
+  return cu > 0 && static_cast<long long>(batch) * heads >= cu;
+}
 
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int max_seq, float scale, int split_size,
-                  float *workspace, hipStream_t stream) {
+                  bool auto_split, float *workspace, hipStream_t stream) {
   const int n_splits = (max_seq + split_size - 1) / split_size;
   const size_t bh = static_cast<size_t>(batch) * heads;
+  if (use_bh_path(batch, heads)) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != FA_OK) return rc;
+    const int cu = device_cu_count(dev);
+    const bool resident = bh <= static_cast<size_t>(bh_blocks_per_cu(dev)) * cu;
+    const int target_waves = resident ? kBhWavesPerCu * cu : 0;
+    if (out_f32)
+      hipLaunchKernelGGL(decode_bh_kernel<true>, dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
+    else
+      hipLaunchKernelGGL(decode_bh_kernel<false>, dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
+    return check_hip(hipGetLastError(), "decode_bh_kernel launch");
+  }
   float *part_acc = workspace;
   float *part_ml = workspace + bh * n_splits * kHeadDim;
   const size_t n_units = bh * n_splits;
@@ -346,6 +574,8 @@ int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
        kSplitThreads},
       {"decode_merge_kernel",
        reinterpret_cast<const void *>(decode_merge_kernel<false>), kMergeThreads},
+      {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<false>),
+       kBhThreads},
   };
   for (const K &k : ks) {
     if (*n < cap) {

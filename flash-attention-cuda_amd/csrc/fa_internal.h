@@ -14,6 +14,7 @@
 namespace fa {
 
 constexpr int kHeadDim = FA_HEAD_DIM;
+constexpr int kMaxDevices = 64;  // per-device host caches
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -41,7 +42,7 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int max_seq, float scale, int split_size,
-                  float *workspace, hipStream_t stream);
+                  bool auto_split, float *workspace, hipStream_t stream);
 
 // Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);

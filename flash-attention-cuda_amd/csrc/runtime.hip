@@ -20,7 +20,8 @@ namespace fa {
 namespace {
 thread_local char g_last_error[512] = "";
 
-constexpr int kMaxDevices = 64;
+// Longest KV cache decode accepts: row indices up to 8x this stay in int.
+constexpr int kMaxCacheRows = 1 << 27;
 std::once_flag g_cu_once[kMaxDevices];
 int g_cu_count[kMaxDevices];
 
@@ -220,10 +221,12 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
   if (batch <= 0 || heads <= 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "batch and heads must be > 0, got B=%d H=%d", batch, heads);
-  if (max_seq <= 0)
-    return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be > 0");
+  if (max_seq <= 0 || max_seq > kMaxCacheRows)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be in [1, %d], got %d",
+                     kMaxCacheRows, max_seq);
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  const bool auto_split = split_size == 0;
   int rc = resolve_split(batch, heads, max_seq, &split_size);
   if (rc != FA_OK) return rc;
   const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
@@ -237,7 +240,7 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
   if (!aligned16(workspace))
     return set_error(FA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   return launch_decode(q, k_cache, v_cache, seq_lens, o, out_dtype == FA_OUT_F32,
-                       batch, heads, max_seq, scale, split_size,
+                       batch, heads, max_seq, scale, split_size, auto_split,
                        static_cast<float *>(workspace),
                        static_cast<hipStream_t>(stream));
 }

@@ -215,6 +215,53 @@ def test_decode_clamps_and_zeroes():
     assert np.abs(out - ref).max() <= BOUND
 
 
+def _ragged_lens(batch, max_seq, seed):
+    """Lengths in [1, max_seq] plus the edge values the kernel must clamp:
+    0, negative, past the cache, exactly the cache, and 1."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, max_seq + 1, (batch,), generator=g, dtype=torch.int32)
+    edges = [0, -3, max_seq + 5, max_seq, 1, 63, 64, 65]
+    lens[: len(edges)] = torch.tensor(edges, dtype=torch.int32)
+    return lens
+
+
+# B * H >= compute units selects the whole-sequence kernel (one block per
+# (b, h)); these shapes cover its resident grid (every block on the chip at
+# once), its oversubscribed grid, and a batch too large for the in-block
+# length ranking.
+WHOLE_SEQUENCE_CASES = [
+    ("resident B32 H14 L700", 32, 14, 700),
+    ("oversubscribed B96 H12 L300", 96, 12, 300),
+    ("unranked B300 H1 L200", 300, 1, 200),
+]
+
+
+@pytest.mark.parametrize("label,batch,heads,max_seq", WHOLE_SEQUENCE_CASES)
+def test_decode_whole_sequence_path_matches_oracle(label, batch, heads, max_seq):
+    lens = _ragged_lens(batch, max_seq, seed=20)
+    q, k, v, lens = oracle.make_decode_inputs(batch, heads, max_seq, seed=21, lens=lens)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    out16 = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+    out32 = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, label)
+    o = out32.cpu().numpy()
+    assert not o[0].any() and not o[1].any()  # len 0 and len < 0: zero rows
+
+
+def test_decode_whole_sequence_split_invariance_fp32():
+    q, k, v, lens = oracle.make_decode_inputs(32, 10, 1500, seed=22,
+                                              lens=_ragged_lens(32, 1500, seed=23))
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    base = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE, 0)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    assert np.abs(base.cpu().numpy() - ref).max() <= BOUND
+    for split in (4, 60, 64, 512, 1500, 4096, 1 << 30):
+        other = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE, split)
+        assert (other - base).abs().max().item() <= 1e-5, split
+
+
 def test_current_stream_is_honoured():
     q, k, v = (t.cuda() for t in oracle.make_prefill_inputs(1, 4, 512, seed=13))
     ref = flashattn_cuda.prefill(q, k, v, True, SCALE)
@@ -233,7 +280,7 @@ def test_occupancy_report_rows():
     rows = flashattn_cuda.occupancy_report()
     names = [r["kernel"] for r in rows]
     assert names == ["prefill_kernel<causal=true>", "prefill_kernel<causal=false>",
-                     "decode_split_kernel", "decode_merge_kernel"]
+                     "decode_split_kernel", "decode_merge_kernel", "decode_bh_kernel"]
     for r in rows:
         assert set(r) == {"kernel", "threads_per_block", "registers_per_thread",
                           "shared_bytes_per_block", "max_active_blocks_per_sm",
