@@ -9,8 +9,9 @@ Prints ONE JSON line on stdout (everything else goes to stderr):
   (B=1, H=14, S=4096, D=64, fp16 in / fp32 accumulate), K timed steps, one
   ``flashattn_cuda.prefill`` call per step, inputs resident in HBM, FLOPs by
   the reference convention 4*B*H*S^2*D/2 (bench/run_bench.py:102-107).
-* ``roofline``: that kernel's achieved TFLOP/s from HIP events around each
-  launch in the timed region, against the dense fp16 MFMA peak.
+* ``roofline``: that kernel's achieved TFLOP/s from a HIP event pair around
+  the K back-to-back launches of the timed region (on the launch stream),
+  against the dense fp16 MFMA peak.
 * ``decode``: BASELINE config 5 (ragged B=32, H=14, Lmax=4096) in GB/s of
   algorithmic bytes (valid K/V rows + q + o + seq_lens) against 8 TB/s, with
   the caches rotated over copies larger than the 256 MB MALL.
@@ -28,7 +29,6 @@ import argparse
 import json
 import math
 import os
-import statistics
 import sys
 import time
 
@@ -107,27 +107,29 @@ def ref_timeit(fn_list, iters=30, warmup=10):
 
 def timed_steps(fn_list, steps, warmup):
     """Contract timing: W untimed steps, then exactly K steps between
-    synchronisations; HIP events around every launch on the launch stream
-    give the kernel's average duration."""
+    synchronisations. A HIP event pair on the launch stream brackets the K
+    back-to-back launches: the host submits a launch in 5-9 us, well under
+    the kernels' duration, so the stream never drains and the event span
+    over K is the kernel's average duration (plus the hardware's
+    kernel-to-kernel gap). Events between launches would instead leave the
+    stream idle for each record call."""
     import torch
 
     n = len(fn_list)
     for i in range(warmup):
         fn_list[i % n]()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(steps):
-        evs[i][0].record(stream)
         fn_list[i % n]()
-        evs[i][1].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    kern_ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
-    return wall_ms / steps, kern_ms
+    return wall_ms / steps, start.elapsed_time(end) / steps
 
 
 def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup=0):
