@@ -17,6 +17,9 @@ Prints ONE JSON line on stdout (everything else goes to stderr):
   the caches rotated over copies larger than the 256 MB MALL.
 * ``configs``: every BASELINE config with the reference's timing protocol
   (10 warm-ups, 3 x 30 launches, median; bench/run_bench.py:83-99).
+* Every timing starts with ~0.1-0.25 s of untimed launches of the same
+  call, which bring the GPU to its sustained clock (an idle MI355X starts
+  lower and needs ~50 ms of load to get there).
 * ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's
   src/attention_cpu.py) timed on this host on a bounded sample of config 3.
 
@@ -85,10 +88,12 @@ def copies_for(nbytes, minimum=1):
 
 def ref_timeit(fn_list, iters=30, warmup=10):
     """bench/run_bench.py:83-99: median of three means over `iters` launches
-    (launch i uses fn_list[i % len(fn_list)] to rotate input copies)."""
+    (launch i uses fn_list[i % len(fn_list)] to rotate input copies), after
+    the clock warm-up below."""
     import torch
 
     n = len(fn_list)
+    clock_warmup(fn_list, 0.1)
     for i in range(warmup):
         fn_list[i % n]()
     torch.cuda.synchronize()
@@ -105,6 +110,23 @@ def ref_timeit(fn_list, iters=30, warmup=10):
     return sorted(samples)[1]
 
 
+def clock_warmup(fn_list, seconds=0.25):
+    """Untimed launches for `seconds` before any timing: an idle MI355X
+    starts below its sustained engine clock and needs ~50 ms of load to reach
+    it (measured: C3 prefill at 73 us in the first 100 launches, 50.5 us from
+    ~1200 launches on), so a short fixed warm-up would time the ramp."""
+    import torch
+
+    n = len(fn_list)
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            fn_list[i % n]()
+            i += 1
+        torch.cuda.synchronize()
+
+
 def timed_steps(fn_list, steps, warmup):
     """Contract timing: W untimed steps, then exactly K steps between
     synchronisations. A HIP event pair on the launch stream brackets the K
@@ -116,6 +138,7 @@ def timed_steps(fn_list, steps, warmup):
     import torch
 
     n = len(fn_list)
+    clock_warmup(fn_list)
     for i in range(warmup):
         fn_list[i % n]()
     stream = torch.cuda.current_stream()
