@@ -43,9 +43,10 @@
 //   LDS reads of the next step's fragments (K_{k+2}, V_k), which land while
 //   the next barrier and row max run.
 //   S and P are double-buffered (the loop is unrolled by two), so the MFMAs of
-//   a step never wait for that step's softmax. Tiles that need a mask (causal
-//   diagonal, ragged tail) and query rows that see fewer than 512 keys take a
-//   plain per-tile step.
+//   a step never wait for that step's softmax. The one tile per half that
+//   needs a mask (causal diagonal, ragged tail) is the pipeline's last step,
+//   with a masked softmax. Blocks whose query rows see fewer than 256 keys
+//   take a plain per-tile step with split P instead.
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
@@ -68,10 +69,11 @@
 // running max, so the dominant key of a row always enters the PV product as
 // P = 1 exactly. The row sum l is accumulated from the same fp16 P values the
 // PV product consumes (v_dot2_f32_f16), so the weights that multiply V sum to
-// exactly the l they are divided by. On tiles that carry a mask and for query
-// rows that see fewer than 512 keys, P is split into hi + lo fp16 parts and
-// the PV product is issued twice: those rows have few, large weights, where
-// one fp16 rounding of P would cost up to ~4e-4 of output accuracy.
+// exactly the l they are divided by. For query rows that see fewer than 256
+// keys, P is split into hi + lo fp16 parts and the PV product is issued
+// twice: those rows have few, large weights, where one fp16 rounding of P
+// would cost up to ~4e-4 of output accuracy (measured with one rounding: 8e-5
+// at >= 256 keys, 1.2e-4 at >= 128 keys).
 
 #include "fa_internal.h"
 
@@ -89,7 +91,7 @@ constexpr int kKStages = 4;
 constexpr int kVStages = 5;
 constexpr int kAhead = 4;                     // tiles in flight ahead of use
 constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per tile
-constexpr int kSplitPRowsBelow = 512;  // rows with fewer keys than this: split P
+constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split P
 constexpr float kNegHuge = -3.0e38f;
 
 // LDS (halves): [Q: 128 rows x 64] [half 0: K ring | V ring] [half 1: ...]
@@ -484,8 +486,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
   // Tiles [0, 2 n_main) need no mask for any row of the block, and all its
   // rows see >= kSplitPRowsBelow keys: each half runs n_main pipelined steps
-  // on them. The rest (causal diagonal, ragged tail, short rows) take the
-  // plain masked step.
+  // on them, then at most one masked pipelined step (n_steps <= n_main + 1
+  // whenever n_main > 0: causal, the diagonal adds two tiles; full, the
+  // ragged tail one). Blocks with short rows take the plain split-P step on
+  // every tile.
   const bool short_rows = CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow;
   const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
   const int n_main = main_tiles / 2;
@@ -577,15 +581,37 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       read_v(ring.vstage(kk + 1), fo, vf);
     }
     // Here step kk - 1 is done: S_kk in s_b, P_{kk-1} in p_a, V_{kk-1} in vf.
-    if (kk < n_main) {  // one more (odd) step: no QK beyond the main tiles
+    // The last step of each half (causal diagonal / ragged tile) runs with a
+    // masked softmax on the S that the previous step's QK produced; waves
+    // that see none of that tile only drain. (Its P is not split: every row
+    // of the block sees >= kSplitPRowsBelow keys.)
+    const bool tail = n_steps == n_main + 1;
+    if (kk < n_main) {  // one more (odd) main step; leaves S_{kk+1} in s_b, P_kk in p_a
       ring.advance(kk);
       rescale_o(st, alpha);
       alpha = tile_max<CAUSAL, false>(s_b, 0, c_scale, st);
+      if (tail) qk_mfma(kf, qf, s_a);
       pv_mfma(vf, p_a, st.o);
-      tile_exp<false, false>(s_b, c_scale, st, p_b, p_unused);
+      tile_exp<false, false>(s_b, c_scale, st, p_a, p_unused);
       read_v(ring.vstage(kk), fo, vf);
+      ++kk;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) s_b[kb] = s_a[kb];
+    }
+    if (tail) {
+      ring.advance(kk);
+      const int key0 = ring.tile(kk) * kBc;
+      const bool active = ring.exists(kk) && key0 < wave_key_end;
       rescale_o(st, alpha);
-      pv_mfma(vf, p_b, st.o);
+      pv_mfma(vf, p_a, st.o);
+      if (active) {
+        const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
+        alpha = tile_max<CAUSAL, true>(s_b, lim, c_scale, st);
+        tile_exp<true, false>(s_b, c_scale, st, p_a, p_unused);
+        read_v(ring.vstage(kk), fo, vf);
+        rescale_o(st, alpha);
+        pv_mfma(vf, p_a, st.o);
+      }
       ++kk;
     } else {
       rescale_o(st, alpha);
@@ -593,7 +619,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     }
   }
 
-  // ---- masked / short-row tiles: one plain step per tile ---------------------
+  // ---- short-row blocks: one plain split-P step per tile ---------------------
   // Tile kk is resident (waited for by an earlier advance, or by the
   // prologue); its fragments are read before the barrier that lets the load
   // of tile kk + 4 overwrite its K stage.
