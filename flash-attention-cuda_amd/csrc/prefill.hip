@@ -435,6 +435,39 @@ struct HalfRing {
   }
 };
 
+// Block -> (b, h) with XCD affinity. The grid stays in level-major order
+// (every head's heaviest query tile first), and blocks go to the 8 XCDs
+// round-robin (block i on XCD i % 8). Head h is "at home" on XCD h % 8:
+// within a level each XCD fills its positions with its home heads first and
+// the leftover heads take the spare positions in a fixed order, so most of a
+// head's blocks share one XCD's L2 (for 14 heads, 89 % of the blocks).
+__device__ __forceinline__ int home_head(int i, int n_bh) {
+  const int level = i / n_bh;
+  const int k = i - level * n_bh;
+  const int base = (level * n_bh) & 7;
+  const int x = (base + k) & 7;     // XCD of this block
+  const int d_x = (x - base) & 7;   // first position of XCD x in this level
+  const int r = (k - d_x) >> 3;     // rank of position k among XCD x's
+  const int nhome_x = (n_bh - x + 7) >> 3;
+  if (r < nhome_x) return x + 8 * r;
+  // A spare position: its index among all spares (XCDs in order, then rank)
+  // selects the matching overflow head (XCDs in order, then head rank).
+  int s = r - nhome_x;
+  for (int y = 0; y < x; ++y) {
+    const int npos = (n_bh - ((y - base) & 7) + 7) >> 3;
+    const int nhome = (n_bh - y + 7) >> 3;
+    s += max(0, npos - nhome);
+  }
+  for (int y = 0; y < 8; ++y) {
+    const int npos = (n_bh - ((y - base) & 7) + 7) >> 3;
+    const int nhome = (n_bh - y + 7) >> 3;
+    const int over = max(0, nhome - npos);
+    if (s < over) return y + 8 * (npos + s);
+    s -= over;
+  }
+  return 0;  // unreachable: spare positions and overflow heads are equal in number
+}
+
 template <bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
@@ -446,7 +479,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // in decreasing work order is a longest-first list schedule.
   const int bh_count = static_cast<int>(gridDim.x) / n_qtiles;
   const int qtile = n_qtiles - 1 - static_cast<int>(blockIdx.x) / bh_count;
-  const int bh = static_cast<int>(blockIdx.x) % bh_count;
+  const int bh = home_head(static_cast<int>(blockIdx.x), bh_count);
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -508,7 +541,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }
 #pragma unroll
   for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
-  wait_loads<0>();
+  // Q and tiles 0, 1 resident (tiles 2, 3 may still be in flight; the first
+  // advance waits for tile 2).
+  if (ring.exists(3))
+    wait_loads<2 * kLoadsPerTile>();
+  else if (ring.exists(2))
+    wait_loads<kLoadsPerTile>();
+  else
+    wait_loads<0>();
   __builtin_amdgcn_s_barrier();
 
   const FragOffsets fo = frag_offsets(lane);
