@@ -112,11 +112,11 @@ int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks) {
   return FA_DECODE_SPLIT_MIN;
 }
 
-// csrc/decode.cu:205-206 sets two split blocks per SM. Here a split-K unit is
-// one wave, and the unit count the chooser aims for is 16 per compute unit
-// (four per SIMD): enough units that the dispatcher keeps every SIMD busy
-// and evens out ragged sequence lengths.
-constexpr int kDecodeUnitsPerCu = 16;
+// csrc/decode.cu:205-206: two split units per compute unit. The split-K path
+// only serves B * H below the compute-unit count, where the longer chunks this
+// target gives measured best (B1 H12 L32768: 25.0 us at 512-row chunks
+// against 39.9 us at 128; short caches pick 128 either way).
+constexpr int kDecodeUnitsPerCu = 2;
 
 int fa_decode_min_blocks(int device, int *min_blocks) {
   clear_error();

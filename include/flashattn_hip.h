@@ -16,8 +16,6 @@
  *                                                 bindings.cpp:122-125
  *   fa_decode_min_blocks     <- min_blocks = 2 * multiProcessorCount
  *                                                 csrc/decode.cu:205-206
- *                               (here 16 * compute units: one split-K unit
- *                               is one wave, not one block)
  *   fa_prefill_workspace_bytes, fa_prefill
  *                            <- launch_prefill    csrc/prefill.cu:347-373
  *                               (called by prefill, bindings.cpp:10-27)
@@ -86,7 +84,7 @@ const char *fa_last_error(void);
 int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks);
 
 /* Split-K unit target the automatic chunk choice uses on `device`:
- * 16 * (compute units); a unit is one wave. Returns an fa_status. */
+ * 2 * (compute units), as the reference. Returns an fa_status. */
 int fa_decode_min_blocks(int device, int *min_blocks);
 
 /* Bytes of device workspace fa_prefill needs for this shape (may be 0). */
