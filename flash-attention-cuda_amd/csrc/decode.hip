@@ -495,7 +495,7 @@ int bh_blocks_per_cu(int device) {
             &n, reinterpret_cast<const void *>(decode_bh_kernel<false>), kBhThreads, 0) !=
             hipSuccess)
       n = 0;
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     blocks[device] = n;
   });
   return blocks[device] > 0 ? blocks[device] : 1;
