@@ -262,6 +262,67 @@ def test_decode_whole_sequence_split_invariance_fp32():
         assert (other - base).abs().max().item() <= 1e-5, split
 
 
+# ---------------------------------------------------------------------------
+# Long sequences and large caches
+# ---------------------------------------------------------------------------
+
+
+def _torch_fp32_attention(q, k, v, causal, scale, rows=2048):
+    """fp32 attention on the GPU, query rows in chunks (contiguous operands)."""
+    qf, kf, vf = q.float(), k.float(), v.float()
+    kt = kf.transpose(-1, -2).contiguous()
+    out = torch.empty_like(qf)
+    seq = q.shape[2]
+    keys = torch.arange(seq, device=q.device)
+    for r0 in range(0, seq, rows):
+        r1 = min(seq, r0 + rows)
+        s = torch.matmul(qf[:, :, r0:r1].contiguous(), kt) * scale
+        if causal:
+            qi = torch.arange(r0, r1, device=q.device).view(-1, 1)
+            s = s.masked_fill(keys.view(1, -1) > qi, float("-inf"))
+        out[:, :, r0:r1] = torch.matmul(torch.softmax(s, dim=-1), vf)
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_long_sequence_matches_fp32_reference(causal):
+    q, k, v = (t.cuda() for t in oracle.make_prefill_inputs(1, 2, 16384, seed=30))
+    ref = _torch_fp32_attention(q, k, v, causal, SCALE)
+    out32 = flashattn_cuda._prefill_fp32(q, k, v, causal, SCALE)
+    out16 = flashattn_cuda.prefill(q, k, v, causal, SCALE)
+    torch.cuda.synchronize()
+    err = (out32 - ref).abs().max().item()
+    print(f"[prefill S16384 causal={causal}] fp32-out err {err:.3e}")
+    assert err <= BOUND
+    assert torch.equal(out16, out32.half())
+
+
+def test_decode_long_cache_split_path():
+    # B * H = 2: the split-K kernels, 64 chunks of 1024 rows per sequence.
+    lens = torch.tensor([65536, 40001], dtype=torch.int32)
+    q, k, v, lens = oracle.make_decode_inputs(2, 1, 65536, seed=31, lens=lens)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    out16 = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+    out32 = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, "decode B2 H1 L65536")
+
+
+@pytest.mark.parametrize("label,batch,heads,max_seq", [
+    ("resident B32 H8 L8192", 32, 8, 8192),
+    ("oversubscribed B192 H4 L2048", 192, 4, 2048),
+])
+def test_decode_large_cache_whole_sequence_path(label, batch, heads, max_seq):
+    q, k, v, lens = oracle.make_decode_inputs(batch, heads, max_seq, seed=32)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    out16 = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+    out32 = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, label)
+
+
 def test_current_stream_is_honoured():
     q, k, v = (t.cuda() for t in oracle.make_prefill_inputs(1, 4, 512, seed=13))
     ref = flashattn_cuda.prefill(q, k, v, True, SCALE)
