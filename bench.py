@@ -20,6 +20,9 @@ Prints ONE JSON line on stdout (everything else goes to stderr):
 * Every timing starts with ~0.1-0.25 s of untimed launches of the same
   call, which bring the GPU to its sustained clock (an idle MI355X starts
   lower and needs ~50 ms of load to get there).
+* ``gqa``: grouped-query prefill / decode (2 K/V heads for 14 query heads)
+  at the config 3 and 5 shapes, beside the repeat-K/V-then-call path the
+  reference's callers use.
 * ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's
   src/attention_cpu.py) timed on this host on a bounded sample of config 3.
 
@@ -189,6 +192,50 @@ def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, war
     step_ms, kern_ms = timed_steps(fns, steps, warmup)
     return {"ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": nbytes, "copies": n,
             "sum_len": int(rl.sum().item())}
+
+
+def bench_gqa(fa):
+    """Grouped-query attention (2 K/V heads for 14 query heads, group 7) at
+    the config 3 and config 5 shapes, reference timing protocol: the kernel
+    entry points (prefill_gqa / decode_gqa) against what the reference's
+    callers do instead, repeat K/V per query head on the device and call
+    prefill / decode. Decode GB/s counts the K/V rows read once per K/V
+    head."""
+    import torch
+
+    rows = []
+    kv_heads, heads = 2, 14
+    group = heads // kv_heads
+    q, k, v = (t.cuda() for t in cpu_inputs_prefill(1, heads, 4096))
+    k2, v2 = k[:, ::group].contiguous(), v[:, ::group].contiguous()
+    torch.cuda.synchronize()
+    flops = attention_flops(1, heads, 4096, True)
+    ms = ref_timeit([lambda: fa.prefill_gqa(q, k2, v2, True, SCALE)])
+    ms_rep = ref_timeit([lambda: fa.prefill(q, k2.repeat_interleave(group, 1),
+                                            v2.repeat_interleave(group, 1), True, SCALE)])
+    rows.append({"config": "C3 GQA causal B1 H14 Hkv2 S4096", "ms": ms,
+                 "tflops": flops / (ms * 1e-3) / 1e12, "ms_repeat_then_prefill": ms_rep})
+    log(f"  {rows[-1]['config']}: {ms * 1e3:.1f} us ({rows[-1]['tflops']:.1f} TFLOP/s); "
+        f"repeat + prefill {ms_rep * 1e3:.1f} us")
+
+    qd, kd, vd, rl = cpu_inputs_decode(32, heads, 4096)
+    kd, vd = kd[:, ::group].contiguous(), vd[:, ::group].contiguous()
+    qd, rl = qd.cuda(), rl.cuda()
+    n = copies_for(2 * kd.numel() * 2)
+    sets = [(kd.cuda(), vd.cuda())]
+    sets += [tuple(t.clone() for t in sets[0]) for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    nbytes = decode_bytes(kv_heads, rl.cpu(), 4096) + 2 * 32 * (heads - kv_heads) * 64 * 2
+    ms = ref_timeit([lambda s=s: fa.decode_gqa(qd, s[0], s[1], rl, SCALE) for s in sets])
+    ms_rep = ref_timeit([lambda s=s: fa.decode(qd, s[0].repeat_interleave(group, 1),
+                                               s[1].repeat_interleave(group, 1), rl, SCALE)
+                         for s in sets])
+    rows.append({"config": "C5 GQA ragged decode B32 H14 Hkv2 Lmax4096", "ms": ms,
+                 "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm": nbytes / (ms * 1e-3) / 1e9 /
+                 HBM_PEAK_GBS, "copies": n, "ms_repeat_then_decode": ms_rep})
+    log(f"  {rows[-1]['config']}: {ms * 1e3:.1f} us ({rows[-1]['gbs']:.1f} GB/s); "
+        f"repeat + decode {ms_rep * 1e3:.1f} us")
+    return rows
 
 
 def cpu_baseline(budget_s=12.0):
@@ -376,6 +423,8 @@ def main():
                          "frac_hbm": r["gbs"] / HBM_PEAK_GBS, "copies": r["copies"]})
             log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['gbs']:.1f} GB/s")
         result["configs"] = rows
+        log("grouped-query attention (no reference counterpart) ...")
+        result["gqa"] = bench_gqa(fa)
 
     if not args.no_cpu:
         log("CPU baseline (oracle, bounded sample) ...")

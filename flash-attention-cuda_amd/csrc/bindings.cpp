@@ -8,8 +8,9 @@
 // contiguous", "head_dim", "identical shapes", "exactly one query row",
 // "seq_lens must be int32", "seq_lens must be 1-D"), output allocation with
 // empty_like(q), asynchronous launch on the current stream, no host sync.
-// Added: a device guard for inputs that live on a non-current device, and
-// the fp32-output parity hooks `_prefill_fp32` / `_decode_fp32`.
+// Added: a device guard for inputs that live on a non-current device, the
+// fp32-output parity hooks `_prefill_fp32` / `_decode_fp32`, and grouped-query
+// variants `prefill_gqa` / `decode_gqa` (K/V with fewer heads than Q).
 //
 // Torch-ROCm calls the HIP device "cuda", so `is_cuda()` is the right check
 // and the reference's messages stay verbatim; the device guard and stream
@@ -50,16 +51,30 @@ void *stream_of(const at::Tensor &t) {
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
 }
 
-// bindings.cpp:10-27.
+// bindings.cpp:10-27. With `grouped`, k and v are [B, H_kv, S, 64] with
+// H_kv dividing H (grouped-query attention, no reference counterpart);
+// otherwise all three shapes must be identical, as in the reference.
 at::Tensor prefill_impl(const at::Tensor &q, const at::Tensor &k,
                         const at::Tensor &v, bool causal, double scale,
-                        bool out_f32) {
+                        bool out_f32, bool grouped = false) {
   check_bhnd(q, "q");
   check_bhnd(k, "k");
   check_bhnd(v, "v");
-  TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
-              "prefill expects q, k and v to have identical shapes, got q=",
-              q.sizes(), " k=", k.sizes(), " v=", v.sizes());
+  if (grouped) {
+    TORCH_CHECK(k.sizes() == v.sizes(),
+                "prefill_gqa expects k and v to have identical shapes, got k=", k.sizes(),
+                " v=", v.sizes());
+    TORCH_CHECK(q.size(0) == k.size(0) && q.size(2) == k.size(2),
+                "prefill_gqa expects q and k/v to agree on batch and sequence length, got q=",
+                q.sizes(), " k=", k.sizes());
+    TORCH_CHECK(k.size(1) > 0 && q.size(1) % k.size(1) == 0,
+                "prefill_gqa expects the K/V head count to divide the query head count, "
+                "got H=", q.size(1), " H_kv=", k.size(1));
+  } else {
+    TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
+                "prefill expects q, k and v to have identical shapes, got q=",
+                q.sizes(), " k=", k.sizes(), " v=", v.sizes());
+  }
   TORCH_CHECK(q.device() == k.device() && q.device() == v.device(),
               "q, k and v must live on the same device");
   TORCH_CHECK(q.size(2) > 0, "sequence length must be > 0");
@@ -75,15 +90,16 @@ at::Tensor prefill_impl(const at::Tensor &q, const at::Tensor &k,
   at::Tensor ws;
   if (ws_bytes > 0)
     ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-  check_status(fa_prefill(q.const_data_ptr(), k.const_data_ptr(),
-                          v.const_data_ptr(), o.data_ptr(),
-                          out_f32 ? FA_OUT_F32 : FA_OUT_F16,
-                          static_cast<int>(q.size(0)),
-                          static_cast<int>(q.size(1)),
-                          static_cast<int>(q.size(2)), causal ? 1 : 0,
-                          static_cast<float>(scale),
-                          ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
-                          stream_of(q)));
+  check_status(fa_prefill_gqa(q.const_data_ptr(), k.const_data_ptr(),
+                              v.const_data_ptr(), o.data_ptr(),
+                              out_f32 ? FA_OUT_F32 : FA_OUT_F16,
+                              static_cast<int>(q.size(0)),
+                              static_cast<int>(q.size(1)),
+                              static_cast<int>(k.size(1)),
+                              static_cast<int>(q.size(2)), causal ? 1 : 0,
+                              static_cast<float>(scale),
+                              ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                              stream_of(q)));
   return o;
 }
 
@@ -97,10 +113,22 @@ at::Tensor prefill_fp32(const at::Tensor &q, const at::Tensor &k,
   return prefill_impl(q, k, v, causal, scale, true);
 }
 
-// bindings.cpp:36-70.
+at::Tensor prefill_gqa(const at::Tensor &q, const at::Tensor &k,
+                       const at::Tensor &v, bool causal, double scale) {
+  return prefill_impl(q, k, v, causal, scale, false, true);
+}
+
+at::Tensor prefill_gqa_fp32(const at::Tensor &q, const at::Tensor &k,
+                            const at::Tensor &v, bool causal, double scale) {
+  return prefill_impl(q, k, v, causal, scale, true, true);
+}
+
+// bindings.cpp:36-70. With `grouped`, the caches are [B, H_kv, Lmax, 64]
+// with H_kv dividing H (no reference counterpart).
 at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
                        const at::Tensor &v_cache, const at::Tensor &seq_lens,
-                       double scale, int64_t split_size, bool out_f32) {
+                       double scale, int64_t split_size, bool out_f32,
+                       bool grouped = false) {
   check_bhnd(q, "q");
   check_bhnd(k_cache, "k_cache");
   check_bhnd(v_cache, "v_cache");
@@ -110,9 +138,17 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
   TORCH_CHECK(k_cache.sizes() == v_cache.sizes(),
               "k_cache and v_cache must have identical shapes, got ",
               k_cache.sizes(), " and ", v_cache.sizes());
-  TORCH_CHECK(q.size(0) == k_cache.size(0) && q.size(1) == k_cache.size(1),
-              "q and the caches must agree on batch and head count, got q=",
-              q.sizes(), " cache=", k_cache.sizes());
+  if (grouped) {
+    TORCH_CHECK(q.size(0) == k_cache.size(0) && k_cache.size(1) > 0 &&
+                    q.size(1) % k_cache.size(1) == 0,
+                "decode_gqa expects q and the caches to agree on batch and the K/V head "
+                "count to divide the query head count, got q=",
+                q.sizes(), " cache=", k_cache.sizes());
+  } else {
+    TORCH_CHECK(q.size(0) == k_cache.size(0) && q.size(1) == k_cache.size(1),
+                "q and the caches must agree on batch and head count, got q=",
+                q.sizes(), " cache=", k_cache.sizes());
+  }
   TORCH_CHECK(k_cache.size(2) > 0, "cache length must be > 0");
 
   TORCH_CHECK(seq_lens.is_cuda(), "seq_lens", " must be a CUDA tensor");
@@ -137,21 +173,22 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
   if (q.numel() == 0) return o;
   const int batch = static_cast<int>(q.size(0));
   const int heads = static_cast<int>(q.size(1));
+  const int kv_heads = static_cast<int>(k_cache.size(1));
   const int max_seq = static_cast<int>(k_cache.size(2));
   const int split = static_cast<int>(split_size);
   const size_t ws_bytes =
-      fa_decode_workspace_bytes(batch, heads, max_seq, split);
+      fa_decode_gqa_workspace_bytes(batch, heads, kv_heads, max_seq, split);
   check_status(ws_bytes > 0 ? FA_OK : FA_ERR_INVALID_ARGUMENT);
   // Transient, stream-ordered workspace from the caching allocator
   // (decode.cu:215-219 of the reference).
   at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes / sizeof(float))},
                             q.options().dtype(at::kFloat));
-  check_status(fa_decode(q.const_data_ptr(), k_cache.const_data_ptr(),
-                         v_cache.const_data_ptr(),
-                         seq_lens.const_data_ptr<int32_t>(), o.data_ptr(),
-                         out_f32 ? FA_OUT_F32 : FA_OUT_F16, batch, heads,
-                         max_seq, static_cast<float>(scale), split,
-                         ws.data_ptr(), ws_bytes, stream_of(q)));
+  check_status(fa_decode_gqa(q.const_data_ptr(), k_cache.const_data_ptr(),
+                             v_cache.const_data_ptr(),
+                             seq_lens.const_data_ptr<int32_t>(), o.data_ptr(),
+                             out_f32 ? FA_OUT_F32 : FA_OUT_F16, batch, heads, kv_heads,
+                             max_seq, static_cast<float>(scale), split,
+                             ws.data_ptr(), ws_bytes, stream_of(q)));
   return o;
 }
 
@@ -172,6 +209,24 @@ at::Tensor decode_fp32(const at::Tensor &q, const at::Tensor &k_cache,
                        const at::Tensor &v_cache, const at::Tensor &seq_lens,
                        double scale, int64_t split_size) {
   return decode_core(q, k_cache, v_cache, seq_lens, scale, split_size, true);
+}
+
+at::Tensor decode_gqa(const at::Tensor &q, const at::Tensor &k_cache,
+                      const at::Tensor &v_cache, const at::Tensor &seq_lens,
+                      double scale) {
+  return decode_core(q, k_cache, v_cache, seq_lens, scale, 0, false, true);
+}
+
+at::Tensor decode_gqa_fp32(const at::Tensor &q, const at::Tensor &k_cache,
+                           const at::Tensor &v_cache, const at::Tensor &seq_lens,
+                           double scale, int64_t split_size) {
+  return decode_core(q, k_cache, v_cache, seq_lens, scale, split_size, true, true);
+}
+
+at::Tensor decode_gqa_with_split(const at::Tensor &q, const at::Tensor &k_cache,
+                                 const at::Tensor &v_cache, const at::Tensor &seq_lens,
+                                 double scale, int64_t split_size) {
+  return decode_core(q, k_cache, v_cache, seq_lens, scale, split_size, false, true);
 }
 
 // bindings.cpp:80-97.
@@ -225,6 +280,25 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_prefill_fp32", &prefill_fp32, py::arg("q"), py::arg("k"),
         py::arg("v"), py::arg("causal"), py::arg("scale"));
   m.def("_decode_fp32", &decode_fp32, py::arg("q"), py::arg("k_cache"),
+        py::arg("v_cache"), py::arg("seq_lens"), py::arg("scale"),
+        py::arg("split_size") = 0);
+
+  // Grouped-query attention (no reference counterpart): k/v (or the caches)
+  // carry H_kv heads, H_kv dividing H; query head h reads K/V head
+  // h / (H / H_kv), the same pairing as repeat_interleave(k, H / H_kv, dim=1).
+  m.def("prefill_gqa", &prefill_gqa,
+        "Full-sequence attention with H_kv <= H K/V heads (fp16 in/out, fp32 accum)",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("scale"));
+  m.def("decode_gqa", &decode_gqa,
+        "Single-query attention against a KV cache with H_kv <= H K/V heads",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("seq_lens"),
+        py::arg("scale"));
+  m.def("_decode_gqa_with_split", &decode_gqa_with_split, py::arg("q"),
+        py::arg("k_cache"), py::arg("v_cache"), py::arg("seq_lens"), py::arg("scale"),
+        py::arg("split_size"));
+  m.def("_prefill_gqa_fp32", &prefill_gqa_fp32, py::arg("q"), py::arg("k"),
+        py::arg("v"), py::arg("causal"), py::arg("scale"));
+  m.def("_decode_gqa_fp32", &decode_gqa_fp32, py::arg("q"), py::arg("k_cache"),
         py::arg("v_cache"), py::arg("seq_lens"), py::arg("scale"),
         py::arg("split_size") = 0);
 }

@@ -36,13 +36,17 @@ int check_hip(hipError_t err, const char *what);
 int device_cu_count(int device);
 
 // ---- kernel launchers (prefill.hip / decode.hip) ---------------------------
+// kv_heads divides heads; query head h reads K/V head h / (heads / kv_heads).
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
-                   bool out_f32, int batch, int heads, int seq, bool causal,
-                   float scale, hipStream_t stream);
+                   bool out_f32, int batch, int heads, int kv_heads, int seq,
+                   bool causal, float scale, hipStream_t stream);
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
-                  int heads, int max_seq, float scale, int split_size,
+                  int heads, int kv_heads, int max_seq, float scale, int split_size,
                   bool auto_split, float *workspace, hipStream_t stream);
+// Decode work units per batch row (one per K/V head and query chunk; one
+// per head without grouped queries): the split chooser's "heads".
+int decode_units_per_row(int heads, int kv_heads);
 
 // Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);

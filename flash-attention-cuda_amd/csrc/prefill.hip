@@ -469,18 +469,30 @@ __device__ __forceinline__ int home_head(int i, int n_bh) {
   return 0;  // unreachable: spare positions and overflow heads are equal in number
 }
 
+// Grouped queries: the placement heads of XCD x (x, x + 8, x + 16, ...) are
+// given a contiguous run of query heads, in XCD order, so the query heads
+// that read one K/V head (consecutive indices) mostly share an XCD and its
+// L2 holds one copy of that K/V head.
+__device__ __forceinline__ int grouped_head(int h, int n_bh) {
+  const int x = h & 7;
+  int start = 0;
+  for (int y = 0; y < x; ++y) start += (n_bh - y + 7) >> 3;
+  return start + (h >> 3);
+}
+
 template <bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
-    int n_qtiles, float c_scale, bool negate_q) {
+    int n_qtiles, int group, float c_scale, bool negate_q) {
   __shared__ __attribute__((aligned(1024))) _Float16 lds[kLdsHalves];
 
   // Heaviest (last) query tiles first: one block fills a CU, so dispatching
   // in decreasing work order is a longest-first list schedule.
   const int bh_count = static_cast<int>(gridDim.x) / n_qtiles;
   const int qtile = n_qtiles - 1 - static_cast<int>(blockIdx.x) / bh_count;
-  const int bh = home_head(static_cast<int>(blockIdx.x), bh_count);
+  int bh = home_head(static_cast<int>(blockIdx.x), bh_count);
+  if (group > 1) bh = grouped_head(bh, bh_count);
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -490,7 +502,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int half = wave / kRowWaves;      // key half: tiles 2k + half
   const int col = lane & 31;
 
+  // Q and O are [B, H, S, 64], K and V [B, H / group, S, 64]: query head
+  // b * H + h reads K/V head b * H / group + h / group = bh / group.
   const size_t head_off = static_cast<size_t>(bh) * seq * kHeadDim;
+  const size_t kv_off = static_cast<size_t>(bh / group) * seq * kHeadDim;
   const int q0 = qtile * kBr;
   const int qw0 = q0 + rw * kRowsPerWave;
   const int my_q = qw0 + col;
@@ -502,8 +517,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   HalfRing ring;
   ring.kring = half_lds;
   ring.vring = half_lds + kKStages * kTileHalves;
-  ring.kp = k + head_off;
-  ring.vp = v + head_off;
+  ring.kp = k + kv_off;
+  ring.vp = v + kv_off;
   ring.seq = seq;
   ring.n_tiles = n_tiles;
   ring.half = half;
@@ -738,35 +753,36 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
 template <bool CAUSAL, bool OUT_F32>
 void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
-                int seq, float c_scale, bool negate_q, hipStream_t stream) {
+                int seq, int group, float c_scale, bool negate_q, hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
   const unsigned blocks = static_cast<unsigned>(bh) * n_qtiles;
   hipLaunchKernelGGL((prefill_kernel<CAUSAL, OUT_F32>), dim3(blocks),
                      dim3(kThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
-                     static_cast<const _Float16 *>(v), o, seq, n_qtiles,
+                     static_cast<const _Float16 *>(v), o, seq, n_qtiles, group,
                      c_scale, negate_q);
 }
 
 }  // namespace
 
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
-                   bool out_f32, int batch, int heads, int seq, bool causal,
-                   float scale, hipStream_t stream) {
+                   bool out_f32, int batch, int heads, int kv_heads, int seq,
+                   bool causal, float scale, hipStream_t stream) {
   const int bh = batch * heads;
+  const int group = heads / kv_heads;
   const float c_scale = fabsf(scale) * kLog2e;
   const bool negate_q = scale < 0.f;
   if (causal) {
     if (out_f32)
-      launch_one<true, true>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
+      launch_one<true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
     else
-      launch_one<true, false>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
+      launch_one<true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
   } else {
     if (out_f32)
-      launch_one<false, true>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
+      launch_one<false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
     else
-      launch_one<false, false>(q, k, v, o, bh, seq, c_scale, negate_q, stream);
+      launch_one<false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
   }
   return check_hip(hipGetLastError(), "prefill_kernel launch");
 }

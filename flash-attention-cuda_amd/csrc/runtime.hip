@@ -132,12 +132,17 @@ int fa_decode_min_blocks(int device, int *min_blocks) {
 
 size_t fa_prefill_workspace_bytes(int, int, int, int) { return 0; }
 
-int fa_prefill(const void *q, const void *k, const void *v, void *o,
-               int out_dtype, int batch, int heads, int seq, int causal,
-               float scale, void *workspace, size_t workspace_bytes,
-               void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
+namespace {
+int check_groups(int heads, int kv_heads) {
+  if (kv_heads <= 0 || kv_heads > heads || heads % kv_heads != 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "kv_heads must divide heads, got H=%d H_kv=%d", heads, kv_heads);
+  return FA_OK;
+}
+
+int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_dtype,
+                 int batch, int heads, int kv_heads, int seq, int causal, float scale,
+                 void *stream) {
   clear_error();
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
     return set_error(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
@@ -149,6 +154,8 @@ int fa_prefill(const void *q, const void *k, const void *v, void *o,
   if (batch <= 0 || heads <= 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "batch and heads must be > 0, got B=%d H=%d", batch, heads);
+  int rc = check_groups(heads, kv_heads);
+  if (rc != FA_OK) return rc;
   if (seq <= 0)
     return set_error(FA_ERR_INVALID_ARGUMENT, "sequence length must be > 0");
   if (static_cast<int64_t>(batch) * heads * ((static_cast<int64_t>(seq) + 127) / 128) >
@@ -156,13 +163,13 @@ int fa_prefill(const void *q, const void *k, const void *v, void *o,
     return set_error(FA_ERR_INVALID_ARGUMENT, "batch * heads * seq too large");
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
-  return launch_prefill(q, k, v, o, out_dtype == FA_OUT_F32, batch, heads, seq,
+  return launch_prefill(q, k, v, o, out_dtype == FA_OUT_F32, batch, heads, kv_heads, seq,
                         causal != 0, scale, static_cast<hipStream_t>(stream));
 }
 
-namespace {
 // Resolves split_size 0 to the automatic choice; returns an fa_status.
-int resolve_split(int batch, int heads, int max_seq, int *split_size) {
+// `units` is the number of decode units per batch row.
+int resolve_split(int batch, int units, int max_seq, int *split_size) {
   if (*split_size < 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "decode split size must be >= 0, got %d", *split_size);
@@ -173,7 +180,7 @@ int resolve_split(int batch, int heads, int max_seq, int *split_size) {
     int min_blocks = 0;
     rc = fa_decode_min_blocks(dev, &min_blocks);
     if (rc != FA_OK) return rc;
-    *split_size = fa_choose_decode_split(max_seq, batch, heads, min_blocks);
+    *split_size = fa_choose_decode_split(max_seq, batch, units, min_blocks);
   }
   // csrc/decode.cu:209-211.
   if (*split_size % 4 != 0)
@@ -188,23 +195,25 @@ size_t decode_ws_bytes(int batch, int heads, int max_seq, int split) {
   return static_cast<size_t>(batch) * heads * n_splits * (FA_HEAD_DIM + 2) *
          sizeof(float);
 }
-}  // namespace
 
-size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
-                                 int split_size) {
+size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq,
+                             int split_size) {
   clear_error();
   if (batch <= 0 || heads <= 0 || max_seq <= 0) {
     set_error(FA_ERR_INVALID_ARGUMENT, "batch, heads and max_seq must be > 0");
     return 0;
   }
-  if (resolve_split(batch, heads, max_seq, &split_size) != FA_OK) return 0;
+  if (check_groups(heads, kv_heads) != FA_OK) return 0;
+  if (resolve_split(batch, decode_units_per_row(heads, kv_heads), max_seq, &split_size) !=
+      FA_OK)
+    return 0;
   return decode_ws_bytes(batch, heads, max_seq, split_size);
 }
 
-int fa_decode(const void *q, const void *k_cache, const void *v_cache,
-              const int32_t *seq_lens, void *o, int out_dtype, int batch,
-              int heads, int max_seq, float scale, int split_size,
-              void *workspace, size_t workspace_bytes, void *stream) {
+int decode_impl(const void *q, const void *k_cache, const void *v_cache,
+                const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
+                int kv_heads, int max_seq, float scale, int split_size, void *workspace,
+                size_t workspace_bytes, void *stream) {
   clear_error();
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       seq_lens == nullptr || o == nullptr)
@@ -221,13 +230,16 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
   if (batch <= 0 || heads <= 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "batch and heads must be > 0, got B=%d H=%d", batch, heads);
+  int rc = check_groups(heads, kv_heads);
+  if (rc != FA_OK) return rc;
   if (max_seq <= 0 || max_seq > kMaxCacheRows)
     return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be in [1, %d], got %d",
                      kMaxCacheRows, max_seq);
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
   const bool auto_split = split_size == 0;
-  int rc = resolve_split(batch, heads, max_seq, &split_size);
+  const int units = decode_units_per_row(heads, kv_heads);
+  rc = resolve_split(batch, units, max_seq, &split_size);
   if (rc != FA_OK) return rc;
   const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
   if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
@@ -240,9 +252,55 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
   if (!aligned16(workspace))
     return set_error(FA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   return launch_decode(q, k_cache, v_cache, seq_lens, o, out_dtype == FA_OUT_F32,
-                       batch, heads, max_seq, scale, split_size, auto_split,
+                       batch, heads, kv_heads, max_seq, scale, split_size, auto_split,
                        static_cast<float *>(workspace),
                        static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+int fa_prefill(const void *q, const void *k, const void *v, void *o,
+               int out_dtype, int batch, int heads, int seq, int causal,
+               float scale, void *workspace, size_t workspace_bytes,
+               void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return prefill_impl(q, k, v, o, out_dtype, batch, heads, heads, seq, causal, scale,
+                      stream);
+}
+
+int fa_prefill_gqa(const void *q, const void *k, const void *v, void *o, int out_dtype,
+                   int batch, int heads, int kv_heads, int seq, int causal, float scale,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, causal, scale,
+                      stream);
+}
+
+size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
+                                 int split_size) {
+  return decode_workspace_impl(batch, heads, heads, max_seq, split_size);
+}
+
+size_t fa_decode_gqa_workspace_bytes(int batch, int heads, int kv_heads, int max_seq,
+                                     int split_size) {
+  return decode_workspace_impl(batch, heads, kv_heads, max_seq, split_size);
+}
+
+int fa_decode(const void *q, const void *k_cache, const void *v_cache,
+              const int32_t *seq_lens, void *o, int out_dtype, int batch,
+              int heads, int max_seq, float scale, int split_size,
+              void *workspace, size_t workspace_bytes, void *stream) {
+  return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, heads,
+                     max_seq, scale, split_size, workspace, workspace_bytes, stream);
+}
+
+int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
+                  const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
+                  int kv_heads, int max_seq, float scale, int split_size, void *workspace,
+                  size_t workspace_bytes, void *stream) {
+  return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, kv_heads,
+                     max_seq, scale, split_size, workspace, workspace_bytes, stream);
 }
 
 int fa_occupancy_report(fa_occupancy_entry *out, int capacity, int *count) {

@@ -6,6 +6,12 @@ shrvan30/flash-attention-cuda): ``prefill``, ``decode``, ``head_dim``,
 benchmark hook, with the same tensor layouts ([B, H, N, 64] fp16 on the
 ``cuda`` device, which is the HIP device on ROCm) and the same errors.
 
+Added beyond the reference: ``prefill_gqa`` and ``decode_gqa``, the same
+kernels for grouped-query attention (k/v or the caches carry H_kv heads, H_kv
+dividing H; query head h reads K/V head h // (H // H_kv), as
+``k.repeat_interleave(H // H_kv, dim=1)`` would pair them), without
+materialising the repeated K/V.
+
 The v1 ``legacy_naive/tiled/fused`` teaching kernels of the reference are
 not part of this build; touching them raises ``NotImplementedError``.
 
@@ -20,13 +26,18 @@ import torch as _torch  # noqa: F401
 try:
     from ._C import (  # noqa: F401
         _decode_fp32,
+        _decode_gqa_fp32,
+        _decode_gqa_with_split,
         _decode_with_split,
         _prefill_fp32,
+        _prefill_gqa_fp32,
         choose_decode_split,
         decode,
+        decode_gqa,
         head_dim,
         occupancy_report,
         prefill,
+        prefill_gqa,
     )
 except ImportError as exc:  # pragma: no cover - exercised only when unbuilt
     raise ImportError(
@@ -47,6 +58,8 @@ legacy_naive = legacy_tiled = legacy_fused = _legacy_unavailable
 __all__ = [
     "prefill",
     "decode",
+    "prefill_gqa",
+    "decode_gqa",
     "head_dim",
     "occupancy_report",
     "choose_decode_split",

@@ -24,6 +24,11 @@
  *                               (called by decode_impl, bindings.cpp:36-76)
  *   fa_occupancy_report      <- prefill_occupancy / decode_occupancy
  *                               csrc/prefill.cu:375-394, csrc/decode.cu:242-261
+ *   fa_prefill_gqa, fa_decode_gqa_workspace_bytes, fa_decode_gqa
+ *                            <- no counterpart: kernel-side grouped-query
+ *                               attention is future work in the reference
+ *                               (README.md:398); its callers repeat K/V per
+ *                               query head and call prefill / decode.
  *
  * Tensor layout (same as the reference): q, k, v, o are [B, H, S, 64]
  * contiguous fp16 (IEEE binary16); a decode cache is [B, H, Lmax, 64]; the
@@ -112,6 +117,28 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
               const int32_t *seq_lens, void *o, int out_dtype, int batch,
               int heads, int max_seq, float scale, int split_size,
               void *workspace, size_t workspace_bytes, void *stream);
+
+/* Grouped-query attention: k and v (or the caches) are [B, H_kv, S, 64]
+ * (or [B, H_kv, Lmax, 64]) with 0 < H_kv <= H and H % H_kv == 0; query head
+ * h reads K/V head h / (H / H_kv), the pairing of
+ * k.repeat_interleave(H / H_kv, dim=1). q and o keep H heads. With
+ * kv_heads == heads these are fa_prefill / fa_decode; otherwise the result
+ * equals theirs on the repeated K/V, which is never materialised (a K/V head
+ * is read once for all of its query heads). Same rules for workspace,
+ * split_size, streams and errors as the non-grouped entry points. */
+int fa_prefill_gqa(const void *q, const void *k, const void *v, void *o,
+                   int out_dtype, int batch, int heads, int kv_heads, int seq,
+                   int causal, float scale, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+size_t fa_decode_gqa_workspace_bytes(int batch, int heads, int kv_heads,
+                                     int max_seq, int split_size);
+
+int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
+                  const int32_t *seq_lens, void *o, int out_dtype, int batch,
+                  int heads, int kv_heads, int max_seq, float scale,
+                  int split_size, void *workspace, size_t workspace_bytes,
+                  void *stream);
 
 /* Fill up to `capacity` entries (one per kernel) for the current device;
  * *count receives the number of kernels. Returns an fa_status. */

@@ -11,10 +11,13 @@ from .attention import (  # noqa: F401
     choose_decode_split,
     decode,
     decode_bytes,
+    decode_gqa,
     fp16_half_ulp,
     fp16_rounding_floor,
     make_decode_inputs,
     make_prefill_inputs,
     prefill,
+    prefill_gqa,
+    repeat_kv,
     stable_softmax,
 )

@@ -18,6 +18,12 @@ What it restates (paths relative to shrvan30/flash-attention-cuda):
 * ``decode``: tests/test_correctness.py:37-44 (per-sequence attention over
   cache rows [:n]) with the kernel's edge semantics from csrc/decode.cu:69
   (n = min(seq_lens[b], Lmax)) and :155-172 (n <= 0 gives a zero output).
+* ``prefill_gqa`` / ``decode_gqa``: grouped-query attention, which the
+  reference leaves to its callers (README.md:398, "Kernel-side GQA (stop
+  paying the host-side KV repeat)"): K/V carry H_kv heads and query head h
+  reads K/V head h // (H // H_kv), the pairing of
+  ``repeat_interleave(H // H_kv, dim=1)``; restated as ``prefill`` /
+  ``decode`` on the repeated K/V.
 * ``choose_decode_split``: csrc/decode.cu:183-192 (integer closed form).
 * ``attention_flops``: bench/run_bench.py:102-107 (4 B H N^2 d, halved when
   causal). ``decode_bytes``: K and V rows actually read plus q, o, seq_lens.
@@ -109,6 +115,28 @@ def decode(q, k_cache, v_cache, seq_lens, scale: float) -> np.ndarray:
         for h in range(H):
             out[b, h] = attention_cpu(q[b, h], k_cache[b, h, :n], v_cache[b, h, :n], scale)
     return out
+
+
+def repeat_kv(x, heads: int) -> np.ndarray:
+    """[B, H_kv, N, 64] -> [B, heads, N, 64]: K/V head g repeated for query
+    heads g * G .. g * G + G - 1 (G = heads // H_kv), as repeat_interleave."""
+    x = np.asarray(x, dtype=np.float32)
+    kv = x.shape[1]
+    if kv <= 0 or heads % kv != 0:
+        raise ValueError(f"H_kv={kv} must divide H={heads}")
+    return np.repeat(x, heads // kv, axis=1)
+
+
+def prefill_gqa(q, k, v, causal: bool, scale: float) -> np.ndarray:
+    """``prefill`` with k, v of shape [B, H_kv, S, 64] (H_kv divides H)."""
+    heads = np.asarray(q).shape[1]
+    return prefill(q, repeat_kv(k, heads), repeat_kv(v, heads), causal, scale)
+
+
+def decode_gqa(q, k_cache, v_cache, seq_lens, scale: float) -> np.ndarray:
+    """``decode`` with caches of shape [B, H_kv, Lmax, 64] (H_kv divides H)."""
+    heads = np.asarray(q).shape[1]
+    return decode(q, repeat_kv(k_cache, heads), repeat_kv(v_cache, heads), seq_lens, scale)
 
 
 def choose_decode_split(max_seq: int, batch: int, heads: int, min_blocks: int) -> int:

@@ -40,6 +40,7 @@ def lib():
     dll.fa_last_error.restype = ctypes.c_char_p
     dll.fa_version.restype = ctypes.c_char_p
     dll.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+    dll.fa_decode_gqa_workspace_bytes.restype = ctypes.c_size_t
     dll.fa_prefill_workspace_bytes.restype = ctypes.c_size_t
     return dll
 
@@ -49,12 +50,15 @@ def test_header_declares_the_expected_entry_points():
         [
             "fa_choose_decode_split",
             "fa_decode",
+            "fa_decode_gqa",
+            "fa_decode_gqa_workspace_bytes",
             "fa_decode_min_blocks",
             "fa_decode_workspace_bytes",
             "fa_head_dim",
             "fa_last_error",
             "fa_occupancy_report",
             "fa_prefill",
+            "fa_prefill_gqa",
             "fa_prefill_workspace_bytes",
             "fa_version",
         ]
@@ -122,12 +126,40 @@ def test_decode_rejects_bad_arguments_before_any_launch(lib):
     assert rc == FA_ERR_INVALID_ARGUMENT and b"scale must be finite" in lib.fa_last_error()
 
 
+def test_grouped_entry_points_check_the_head_grouping(lib):
+    """kv_heads must be in (0, heads] and divide heads; checked before any launch."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    f = ctypes.c_float
+    sz = ctypes.c_size_t
+    for kv in (0, -2, 3, 16):
+        rc = lib.fa_prefill_gqa(p, p, p, p, 0, 1, 8, kv, 8, 1, f(0.125), None, sz(0), None)
+        assert rc == FA_ERR_INVALID_ARGUMENT and b"kv_heads must divide heads" in lib.fa_last_error()
+        rc = lib.fa_decode_gqa(p, p, p, p, p, 0, 1, 8, kv, 8, f(0.125), 128, p, sz(1 << 16), None)
+        assert rc == FA_ERR_INVALID_ARGUMENT and b"kv_heads must divide heads" in lib.fa_last_error()
+        assert lib.fa_decode_gqa_workspace_bytes(1, 8, kv, 4096, 128) == 0
+    # The other checks are shared with the non-grouped entry points.
+    rc = lib.fa_prefill_gqa(p, p, p, p, 0, 1, 8, 2, 0, 1, f(0.125), None, sz(0), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"sequence length must be > 0" in lib.fa_last_error()
+    rc = lib.fa_decode_gqa(p, p, p, p, p, 0, 1, 8, 2, 8, f(0.125), 128, p, sz(16), None)
+    assert rc == FA_ERR_WORKSPACE and b"workspace too small" in lib.fa_last_error()
+
+
+def test_grouped_decode_workspace_holds_one_partial_per_query_head(lib):
+    # A forced split: partials are per query head, as without grouping.
+    assert lib.fa_decode_gqa_workspace_bytes(32, 14, 2, 4096, 1024) == 32 * 14 * 4 * 66 * 4
+    assert lib.fa_decode_gqa_workspace_bytes(32, 14, 14, 4096, 1024) == \
+        lib.fa_decode_workspace_bytes(32, 14, 4096, 1024)
+    assert lib.fa_decode_gqa_workspace_bytes(1, 12, 4, 4096, 128) == 12 * 32 * 66 * 4
+
+
 def test_python_package_exposes_reference_surface():
     """flashattn_cuda/__init__.py:20-29 of the reference (legacy_* stubbed)."""
     import flashattn_cuda as fa
 
     for name in ("prefill", "decode", "head_dim", "occupancy_report", "choose_decode_split",
-                 "_decode_with_split", "legacy_naive", "legacy_tiled", "legacy_fused"):
+                 "_decode_with_split", "legacy_naive", "legacy_tiled", "legacy_fused",
+                 "prefill_gqa", "decode_gqa"):
         assert hasattr(fa, name), name
     assert fa.head_dim == 64 and fa.__version__ == "2.0.0"
     assert fa.choose_decode_split(512, 1, 12, 512) == 128

@@ -1,0 +1,282 @@
+"""Grouped-query attention: ``prefill_gqa`` / ``decode_gqa`` and their C ABI.
+
+The reference leaves GQA to its callers, which repeat K/V per query head on
+the host and call ``prefill`` / ``decode`` (README.md:398 lists kernel-side
+GQA as future work). These entry points take K/V with H_kv heads and must
+give the result of the reference's path on the repeated K/V:
+
+* against the oracle (``oracle.prefill_gqa`` / ``decode_gqa``, pinned in
+  tests/test_oracle.py) within the 2.44e-4 bound of the non-grouped path;
+* against this library's own ``prefill`` / ``decode`` on the repeated K/V
+  (bit-exact for prefill, whose per-block arithmetic does not depend on the
+  grouping; within 1e-5 in fp32 for decode, whose grouped units fold rows in
+  other sub-step sizes);
+* for every queries-per-unit count (1..8) on both decode paths (split-K and
+  whole-sequence), with ragged and edge lengths.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import flashattn_cuda
+import oracle
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+BOUND = 2.44e-4
+SCALE = 0.125
+LIB = os.path.join(os.path.dirname(flashattn_cuda.__file__), "libflashattn_hip.so")
+
+
+def _cu_count():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def _queries_per_unit(group):
+    return max(d for d in range(1, 9) if group % d == 0)
+
+
+def _units(batch, heads, kv_heads):
+    group = heads // kv_heads
+    return batch * kv_heads * (group // _queries_per_unit(group))
+
+
+def _rand(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).half()
+
+
+def _check(out16, out32, ref, label):
+    ref = np.asarray(ref, dtype=np.float64)
+    o32 = out32.float().cpu().numpy().astype(np.float64)
+    o16 = out16.float().cpu().numpy().astype(np.float64)
+    err32 = float(np.abs(o32 - ref).max())
+    slack = float((np.abs(o16 - ref) - orc.fp16_half_ulp(ref)).max())
+    print(f"[{label}] fp32-out err {err32:.3e} | fp16 excess over half-ulp {slack:.3e}", flush=True)
+    assert err32 <= BOUND, f"{label}: fp32-output error {err32}"
+    assert slack <= BOUND, f"{label}: fp16-output error beyond rounding {slack}"
+    assert torch.equal(out16.cpu(), out32.half().cpu()), f"{label}: fp16 != rn(fp32)"
+
+
+def _repeat(x, heads):
+    return x.repeat_interleave(heads // x.shape[1], dim=1).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Prefill
+# ---------------------------------------------------------------------------
+
+PREFILL_CASES = [
+    ("B2 H8 Hkv2 S333 causal", 2, 8, 2, 333, True),
+    ("B2 H8 Hkv2 S333 full", 2, 8, 2, 333, False),
+    ("B1 H14 Hkv2 S1024 causal", 1, 14, 2, 1024, True),
+    ("B3 H12 Hkv1 S200 full (multi-query)", 3, 12, 1, 200, False),
+    ("B1 H32 Hkv8 S512 causal", 1, 32, 8, 512, True),
+    ("B2 H6 Hkv6 S130 causal (no grouping)", 2, 6, 6, 130, True),
+]
+
+
+@pytest.mark.parametrize("label,batch,heads,kv_heads,seq,causal", PREFILL_CASES)
+def test_prefill_gqa_matches_oracle_and_repeated_prefill(label, batch, heads, kv_heads, seq,
+                                                          causal):
+    print(f"[prefill_gqa] {label}", flush=True)
+    q = _rand((batch, heads, seq, 64), 100)
+    k = _rand((batch, kv_heads, seq, 64), 101)
+    v = _rand((batch, kv_heads, seq, 64), 102)
+    ref = oracle.prefill_gqa(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out16 = flashattn_cuda.prefill_gqa(qd, kd, vd, causal, SCALE)
+    out32 = flashattn_cuda._prefill_gqa_fp32(qd, kd, vd, causal, SCALE)
+    rep = flashattn_cuda._prefill_fp32(qd, _repeat(kd, heads), _repeat(vd, heads), causal, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, label)
+    assert torch.equal(out32, rep), f"{label}: differs from prefill on the repeated K/V"
+
+
+def test_prefill_gqa_c3_shape_against_repeated_prefill():
+    """The C3 shape (B1 H14 S4096 causal) with 2 K/V heads, bit-exact."""
+    q = _rand((1, 14, 4096, 64), 103).cuda()
+    k = _rand((1, 2, 4096, 64), 104).cuda()
+    v = _rand((1, 2, 4096, 64), 105).cuda()
+    got = flashattn_cuda.prefill_gqa(q, k, v, True, SCALE)
+    rep = flashattn_cuda.prefill(q, _repeat(k, 14), _repeat(v, 14), True, SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(got, rep)
+
+
+def test_prefill_gqa_rejects_bad_groupings():
+    q = torch.zeros(1, 6, 8, 64, dtype=torch.float16, device="cuda")
+    k = torch.zeros(1, 4, 8, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="divide the query head count"):
+        flashattn_cuda.prefill_gqa(q, k, k, True, SCALE)
+    with pytest.raises(RuntimeError, match="identical shapes"):
+        flashattn_cuda.prefill_gqa(q, k[:, :3], k[:, :2].contiguous(), True, SCALE)
+    with pytest.raises(RuntimeError, match="batch and sequence length"):
+        flashattn_cuda.prefill_gqa(q, k[:, :3, :4].contiguous(), k[:, :3, :4].contiguous(),
+                                   True, SCALE)
+    # The reference's entry point keeps its strict identical-shape check.
+    with pytest.raises(RuntimeError, match="identical shapes"):
+        flashattn_cuda.prefill(q, k[:, :3].contiguous(), k[:, :3].contiguous(), True, SCALE)
+
+
+# ---------------------------------------------------------------------------
+# Decode
+# ---------------------------------------------------------------------------
+
+
+def _ragged_lens(batch, max_seq, seed):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, max_seq + 1, (batch,), generator=g, dtype=torch.int32)
+    edges = [0, -3, max_seq + 5, max_seq, 1, 63, 64, 65]
+    n = min(batch, len(edges))
+    lens[:n] = torch.tensor(edges[:n], dtype=torch.int32)
+    return lens
+
+
+def _decode_case(batch, heads, kv_heads, max_seq, seed):
+    lens = _ragged_lens(batch, max_seq, seed)
+    q = _rand((batch, heads, 1, 64), seed + 1)
+    k = _rand((batch, kv_heads, max_seq, 64), seed + 2)
+    v = _rand((batch, kv_heads, max_seq, 64), seed + 3)
+    return q, k, v, lens
+
+
+def _run_decode(label, batch, heads, kv_heads, max_seq, seed, split=0):
+    q, k, v, lens = _decode_case(batch, heads, kv_heads, max_seq, seed)
+    ref = oracle.decode_gqa(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    out32 = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE, split)
+    out16 = (flashattn_cuda.decode_gqa(qd, kd, vd, ld, SCALE) if split == 0 else
+             flashattn_cuda._decode_gqa_with_split(qd, kd, vd, ld, SCALE, split))
+    rep = flashattn_cuda._decode_fp32(qd, _repeat(kd, heads), _repeat(vd, heads), ld, SCALE,
+                                      split)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, label)
+    diff = (out32 - rep).abs().max().item()
+    assert diff <= 1e-5, f"{label}: {diff} from decode on the repeated caches"
+    o = out32.cpu().numpy()
+    assert not o[0].any()
+    if batch > 1:
+        assert not o[1].any()  # len 0 and len < 0: zero rows
+
+
+# group -> NQ: 2->2, 3->3, 4->4, 5->5, 6->6, 7->7, 8->8, 14->7 (2 units per
+# K/V head), 16->8 (2 units), 9->3 (3 units).
+GROUPS = [2, 3, 4, 5, 6, 7, 8, 14, 16, 9]
+
+
+@pytest.mark.parametrize("group", GROUPS)
+def test_decode_gqa_split_path(group):
+    batch, kv_heads, max_seq = 3, 2, 1500
+    assert _units(batch, group * kv_heads, kv_heads) < _cu_count()
+    _run_decode(f"split path B3 Hkv2 G{group} L1500", batch, group * kv_heads, kv_heads,
+                max_seq, seed=200 + group)
+
+
+@pytest.mark.parametrize("group", GROUPS)
+def test_decode_gqa_whole_sequence_path(group):
+    kv_heads, max_seq = 2, 300
+    nq_units = kv_heads * (group // _queries_per_unit(group))
+    batch = -(-_cu_count() // nq_units) + 1  # just past one unit per CU
+    assert _units(batch, group * kv_heads, kv_heads) >= _cu_count()
+    _run_decode(f"whole-sequence B{batch} Hkv2 G{group} L300", batch, group * kv_heads,
+                kv_heads, max_seq, seed=300 + group)
+
+
+def test_decode_gqa_oversubscribed_and_unranked():
+    """More blocks than fit at once, and a batch past the in-block ranking."""
+    _run_decode("oversubscribed B160 H16 Hkv4 L400", 160, 16, 4, 400, seed=400)
+    _run_decode("unranked B300 H4 Hkv1 L120", 300, 4, 1, 120, seed=401)
+
+
+def test_decode_gqa_c5_shape():
+    """The C5 batch (B32 H14 Lmax4096, ragged) with 2 K/V heads (group 7)."""
+    q, k, v, lens = oracle.make_decode_inputs(32, 14, 4096, seed=0)
+    k2, v2 = k[:, ::7].contiguous(), v[:, ::7].contiguous()
+    ref = oracle.decode_gqa(q.numpy(), k2.numpy(), v2.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k2.cuda(), v2.cuda(), lens.cuda()
+    out16 = flashattn_cuda.decode_gqa(qd, kd, vd, ld, SCALE)
+    out32 = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, "C5 GQA B32 H14 Hkv2 Lmax4096")
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (14, 2)])
+def test_decode_gqa_split_invariance_fp32(heads, kv_heads):
+    q, k, v, lens = _decode_case(4, heads, kv_heads, 2000, seed=500)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    base = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE, 0)
+    for split in (4, 64, 128, 1000, 1024, 4096):
+        other = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE, split)
+        assert (other - base).abs().max().item() <= 1e-5, split
+
+
+def test_decode_gqa_one_group_equals_decode():
+    q, k, v, lens = oracle.make_decode_inputs(5, 3, 700, seed=501)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    torch.cuda.synchronize()
+    assert torch.equal(flashattn_cuda.decode_gqa(qd, kd, vd, ld, SCALE),
+                       flashattn_cuda.decode(qd, kd, vd, ld, SCALE))
+
+
+def test_decode_gqa_rejects_bad_groupings():
+    q = torch.zeros(2, 6, 1, 64, dtype=torch.float16, device="cuda")
+    cache = torch.zeros(2, 4, 16, 64, dtype=torch.float16, device="cuda")
+    lens = torch.full((2,), 8, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="divide the query head count"):
+        flashattn_cuda.decode_gqa(q, cache, cache, lens, SCALE)
+    with pytest.raises(RuntimeError, match="agree on batch"):
+        flashattn_cuda.decode_gqa(q, cache[:1, :3].contiguous(), cache[:1, :3].contiguous(),
+                                  lens, SCALE)
+    with pytest.raises(RuntimeError, match="agree on batch and head count"):
+        flashattn_cuda.decode(q, cache[:, :3].contiguous(), cache[:, :3].contiguous(), lens,
+                              SCALE)
+
+
+# ---------------------------------------------------------------------------
+# C ABI
+# ---------------------------------------------------------------------------
+
+
+@pytest.fixture(scope="module")
+def capi():
+    dll = ctypes.CDLL(LIB)
+    dll.fa_last_error.restype = ctypes.c_char_p
+    dll.fa_decode_gqa_workspace_bytes.restype = ctypes.c_size_t
+    return dll
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def test_capi_prefill_gqa_matches_python_api(capi):
+    q = _rand((2, 6, 333, 64), 600).cuda()
+    k = _rand((2, 2, 333, 64), 601).cuda()
+    v = _rand((2, 2, 333, 64), 602).cuda()
+    o = torch.empty_like(q)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = capi.fa_prefill_gqa(_p(q), _p(k), _p(v), _p(o), 0, 2, 6, 2, 333, 1,
+                             ctypes.c_float(SCALE), None, ctypes.c_size_t(0), stream)
+    assert rc == 0, capi.fa_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(o, flashattn_cuda.prefill_gqa(q, k, v, True, SCALE))
+
+
+def test_capi_decode_gqa_matches_python_api(capi):
+    q, k, v, lens = (t.cuda() for t in _decode_case(3, 8, 2, 700, seed=603))
+    o = torch.empty_like(q)
+    ws_bytes = capi.fa_decode_gqa_workspace_bytes(3, 8, 2, 700, 0)
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes // 4 + 4, dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = capi.fa_decode_gqa(_p(q), _p(k), _p(v), _p(lens), _p(o), 0, 3, 8, 2, 700,
+                            ctypes.c_float(SCALE), 0, _p(ws), ctypes.c_size_t(ws_bytes), stream)
+    assert rc == 0, capi.fa_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(o, flashattn_cuda.decode_gqa(q, k, v, lens, SCALE))

@@ -317,3 +317,69 @@ def test_planted_decode_mistakes_are_caught(kind):
 
     with pytest.raises(AssertionError):
         check_decode_fn(bad_decode)
+
+
+# ---------------------------------------------------------------------------
+# Grouped-query attention: query head h reads K/V head h // G.
+# ---------------------------------------------------------------------------
+
+
+def _gqa_loop(q, k, v, causal, scale):
+    """fp64 brute force written per query head with an explicit K/V index."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    B, H, N, _ = q.shape
+    G = H // k.shape[1]
+    out = np.zeros(q.shape)
+    for b in range(B):
+        for h in range(H):
+            g = h // G
+            for i in range(N):
+                n_keys = i + 1 if causal else k.shape[2]
+                s = [scale * float(q[b, h, i] @ k[b, g, j]) for j in range(n_keys)]
+                mx = max(s)
+                w = [math.exp(x - mx) for x in s]
+                out[b, h, i] = sum(wj * v[b, g, j] for j, wj in enumerate(w)) / sum(w)
+    return out
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (6, 1), (6, 3), (3, 3)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_gqa_matches_explicit_head_loop(heads, kv_heads, causal):
+    q = _rand((2, heads, 9, 64), 40)
+    k = _rand((2, kv_heads, 9, 64), 41)
+    v = _rand((2, kv_heads, 9, 64), 42)
+    got = oracle.prefill_gqa(q, k, v, causal, 0.125)
+    assert np.abs(got - _gqa_loop(q, k, v, causal, 0.125)).max() < 2e-6
+
+
+def test_gqa_with_one_group_is_plain_attention_and_pairing_is_interleaved():
+    q = _rand((1, 6, 7, 64), 43).numpy()
+    k = _rand((1, 6, 7, 64), 44).numpy()
+    v = _rand((1, 6, 7, 64), 45).numpy()
+    assert np.array_equal(oracle.prefill_gqa(q, k, v, True, 0.125), oracle.prefill(q, k, v, True, 0.125))
+    # torch's repeat_interleave is the pairing; torch's tile-style repeat
+    # (head h reads K/V head h % H_kv) is a planted mistake it must reject.
+    k2, v2 = k[:, :2], v[:, :2]
+    kt = torch.from_numpy(k2).repeat_interleave(3, dim=1).numpy()
+    assert np.array_equal(oracle.repeat_kv(k2, 6), kt)
+    tiled = oracle.prefill(q, np.tile(k2, (1, 3, 1, 1)), np.tile(v2, (1, 3, 1, 1)), True, 0.125)
+    good = oracle.prefill_gqa(q, k2, v2, True, 0.125)
+    assert np.abs(tiled - good).max() > 1e-2
+    assert np.abs(good - _gqa_loop(q, k2, v2, True, 0.125)).max() < 2e-6
+    with pytest.raises(ValueError):
+        oracle.repeat_kv(k[:, :4], 6)
+
+
+def test_decode_gqa_equals_causal_prefill_gqa_row():
+    q = _rand((2, 8, 12, 64), 46)
+    k = _rand((2, 2, 12, 64), 47)
+    v = _rand((2, 2, 12, 64), 48)
+    full = oracle.prefill_gqa(q, k, v, True, 0.125)
+    for t in (0, 5, 11):
+        lens = np.full(2, t + 1, dtype=np.int32)
+        got = oracle.decode_gqa(q[:, :, t : t + 1], k, v, lens, 0.125)
+        assert np.abs(got - full[:, :, t : t + 1]).max() < 2e-6
+    lens = np.array([0, 30], dtype=np.int32)  # empty, and clamped to the cache
+    got = oracle.decode_gqa(q[:, :, 11:12], k, v, lens, 0.125)
+    assert not got[0].any()
+    assert np.abs(got[1] - full[1, :, 11:12]).max() < 2e-6

@@ -391,3 +391,28 @@ def test_capi_decode_matches_python_api(capi):
     min_blocks = ctypes.c_int(0)
     assert capi.fa_decode_min_blocks(0, ctypes.byref(min_blocks)) == 0
     assert min_blocks.value == 2 * torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def test_capi_decode_ignores_stale_workspace_contents(capi):
+    """The merge pass reads the first 8 partial slots before it knows how many
+    chunks hold rows; slots of empty chunks are never written in this call.
+    A workspace full of NaN (stale bits from an earlier use) must not leak
+    into the output."""
+    lens = torch.tensor([1, 130, 700, 3000], dtype=torch.int32)
+    q, k, v, lens = oracle.make_decode_inputs(4, 2, 4096, seed=16, lens=lens)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    q, k, v, lens = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    o = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    split = 128  # 32 chunks per sequence; the short ones leave most slots unwritten
+    ws_bytes = capi.fa_decode_workspace_bytes(4, 2, 4096, split)
+    ws = torch.full((ws_bytes // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = capi.fa_decode(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
+                        ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(lens.data_ptr()),
+                        ctypes.c_void_p(o.data_ptr()), 1, 4, 2, 4096, ctypes.c_float(SCALE),
+                        split, ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws_bytes), stream)
+    assert rc == 0, capi.fa_last_error()
+    torch.cuda.synchronize()
+    out = o.cpu().numpy()
+    assert np.isfinite(out).all()
+    assert np.abs(out - ref).max() <= BOUND
