@@ -40,10 +40,12 @@
 
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
 #include "fa_internal.h"
+#include "mfma_tile.h"
 
 namespace fa {
 namespace {
@@ -98,63 +100,61 @@ __device__ __forceinline__ void unpack8(const uint4 &raw, float f[8]) {
   }
 }
 
-// Fold one sub-step of rows (already loaded) into the running states of the
-// NQ queries that share this K/V head (NQ = 1 without grouped queries). The
+// Fold one sub-step of rows (already loaded) into the running state. The
 // q.k partial of a lane is four v_dot2_f32_f16 on the raw fp16 pairs (exact
-// fp16 products, fp32 sums), scaled once by qscale = scale * log2(e); each V
-// row is unpacked once and feeds every query's accumulator.
-template <int G, int NQ>
-__device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r,
-                                              const half2 (&qh)[NQ][4], float qscale,
-                                              int row0, int end, int sub, float (&m)[NQ],
-                                              float (&l)[NQ], float (&acc)[NQ][8]) {
-  float s[NQ][G];
+// fp16 products, fp32 sums), scaled once by qscale = scale * log2(e).
+template <int G>
+__device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r, const half2 (&qh)[4],
+                                              float qscale, int row0, int end, int sub,
+                                              float &m, float &l, float (&acc)[8]) {
+  float s[G];
 #pragma unroll
   for (int u = 0; u < G; ++u) {
     const half2 *kh = reinterpret_cast<const half2 *>(&r.k[u]);
+    float part = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) part = __builtin_amdgcn_fdot2(qh[t], kh[t], part, false);
+    part = sum_lanes8(part);
     const int row = row0 + u * kRowsPerGroup + sub;
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      float part = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) part = __builtin_amdgcn_fdot2(qh[j][t], kh[t], part, false);
-      part = sum_lanes8(part);
-      s[j][u] = (row < end) ? part * qscale : -INFINITY;
-    }
+    s[u] = (row < end) ? part * qscale : -INFINITY;
   }
-  float p[NQ][G];
+  float mx = s[0];
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    float mx = s[j][0];
+  for (int u = 1; u < G; ++u) mx = fmaxf(mx, s[u]);
+  const float m_new = fmaxf(m, mx);
+  const float alpha = fast_exp2(m - m_new);
+  float p[G];
+  float psum = 0.f;
 #pragma unroll
-    for (int u = 1; u < G; ++u) mx = fmaxf(mx, s[j][u]);
-    const float m_new = fmaxf(m[j], mx);
-    const float alpha = fast_exp2(m[j] - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      p[j][u] = fast_exp2(s[j][u] - m_new);  // masked rows: exp2(-inf) = 0
-      psum += p[j][u];
-    }
-    l[j] = fmaf(l[j], alpha, psum);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
-    m[j] = m_new;
+  for (int u = 0; u < G; ++u) {
+    p[u] = fast_exp2(s[u] - m_new);  // masked rows: exp2(-inf) = 0
+    psum += p[u];
   }
+  l = fmaf(l, alpha, psum);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
   for (int u = 0; u < G; ++u) {
     float vf[8];
     unpack8(r.v[u], vf);
 #pragma unroll
-    for (int j = 0; j < NQ; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(p[j][u], vf[e], acc[j][e]);
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(p[u], vf[e], acc[e]);
   }
+  m = m_new;
 }
 
-// Query j of a query unit: the NQ query heads that read one K/V head.
-// The unit index u runs over (b, kv head, query chunk); query j is head
-// kv * group + chunk * NQ + j of batch row b.
+// Head dims [8 * slice, +8) of query row bh, as fp16 pairs.
+__device__ __forceinline__ void load_query(const _Float16 *q, size_t bh, int slice,
+                                           half2 (&qh)[4]) {
+  const uint4 raw = *reinterpret_cast<const uint4 *>(q + bh * kHeadDim + slice * 8);
+  const half2 *h = reinterpret_cast<const half2 *>(&raw);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) qh[t] = h[t];
+}
+
+// A grouped-query unit: nq query heads that read one K/V head. The unit index
+// u runs over (b, K/V head, query chunk); its queries are heads
+// kv * group + chunk * nq + j (j < nq) of batch row b.
 struct QueryUnit {
   int b, kv, h0;
 };
@@ -167,19 +167,6 @@ __device__ __forceinline__ QueryUnit query_unit(int u, int kv_heads, int q_chunk
   r.kv = rest / q_chunks;
   r.h0 = r.kv * group + (rest - r.kv * q_chunks) * nq;
   return r;
-}
-
-// The 8 head dims [8 * slice, +8) of each of the NQ queries, as fp16 pairs.
-template <int NQ>
-__device__ __forceinline__ void load_queries(const _Float16 *q, size_t bh0, int slice,
-                                             half2 (&qh)[NQ][4]) {
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    const uint4 raw = *reinterpret_cast<const uint4 *>(q + (bh0 + j) * kHeadDim + slice * 8);
-    const half2 *h = reinterpret_cast<const half2 *>(&raw);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) qh[j][t] = h[t];
-  }
 }
 
 // Merge state (mb, lb, accb) into (m, l, acc); both in the log2 domain.
@@ -196,28 +183,25 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
 }
 
 // Pass 1 (decode.cu:50-138): one wave folds cache rows
-// [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one K/V head into a
-// partial (m, l, acc[64]) for each of the NQ query heads that read it. Unit
-// w = chunk_i * n_qu + u (u over (b, kv head, query chunk)) is handled by
-// wave w % 4 of block w / 4. G row groups (8 rows each) are loaded per
-// sub-step.
-template <int G, int NQ>
+// [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
+// partial (m, l, acc[64]). Unit u = chunk_i * (B * H) + (b * H + h) is
+// handled by wave u % 4 of block u / 4.
 __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
     float *__restrict__ part_acc, float *__restrict__ part_ml, int heads,
-    int kv_heads, int group, int max_seq, int n_splits, int n_units, int chunk,
-    float qscale) {
+    int max_seq, int n_splits, int n_units, int chunk, float qscale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int unit = static_cast<int>(blockIdx.x) * kSplitWaves +
                    __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   if (unit >= n_units) return;
-  // Chunk-major order: every unit's first chunk is dispatched first, its
+  // Chunk-major order: every (b, h)'s first chunk is dispatched first, its
   // last chunks (empty for short sequences) last, so the hardware dispatcher
   // hands out the heaviest units first (a longest-first list schedule).
-  const int n_qu = n_units / n_splits;
-  const int split = unit / n_qu;
-  const QueryUnit qu = query_unit(unit - split * n_qu, kv_heads, group / NQ, group, NQ);
+  const int n_bh = n_units / n_splits;
+  const int split = unit / n_bh;
+  const int bh = unit % n_bh;
+  const int b = bh / heads;
 
   const int sub = lane >> 3;   // row inside an 8-row group
   const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
@@ -225,35 +209,28 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   // decode.cu:69-71: clamp to the cache capacity. A chunk past the sequence
   // end has no rows: it writes nothing, and the merge pass only reads the
   // partials of the ceil(len / chunk) chunks that have rows.
-  const int len = min(seq_lens[qu.b], max_seq);
+  const int len = min(seq_lens[b], max_seq);
   const int begin = split * chunk;
   if (begin >= len) return;
   const int end = min(len, begin + chunk);
 
-  const size_t kv_off =
-      (static_cast<size_t>(qu.b) * kv_heads + qu.kv) * max_seq * kHeadDim;
-  const _Float16 *kp = k_cache + kv_off;
-  const _Float16 *vp = v_cache + kv_off;
-  const size_t bh0 = static_cast<size_t>(qu.b) * heads + qu.h0;
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const _Float16 *kp = k_cache + head_off;
+  const _Float16 *vp = v_cache + head_off;
 
   // Double-buffered row slots: the loads of sub-step i+1 are in flight while
   // sub-step i is consumed.
-  constexpr int kStepRows = kRowsPerGroup * G;
-  RowSlotsT<G> cur, nxt;
+  constexpr int kStepRows = kRowsPerGroup * kGroupsPerStep;
+  RowSlotsT<kGroupsPerStep> cur, nxt;
   int row0 = begin;
   load_slots(cur, kp, vp, row0, end, sub, slice);
 
-  half2 qh[NQ][4];
-  load_queries<NQ>(q, bh0, slice, qh);
+  half2 qh[4];
+  load_query(q, bh, slice, qh);
 
-  float m[NQ], l[NQ], acc[NQ][8];
+  float m = kNegBig, l = 0.f, acc[8];
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    m[j] = kNegBig;
-    l[j] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  }
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
   for (;;) {
     const int next0 = row0 + kStepRows;
@@ -265,25 +242,23 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     row0 = next0;
   }
 
+  // Merge the 8 row groups of the wave (lanes that share `slice`).
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    // Merge the 8 row groups of the wave (lanes that share `slice`).
+  for (int off = 8; off < kWave; off <<= 1) {
+    const float mb = __shfl_xor(m, off);
+    const float lb = __shfl_xor(l, off);
+    float accb[8];
 #pragma unroll
-    for (int off = 8; off < kWave; off <<= 1) {
-      const float mb = __shfl_xor(m[j], off);
-      const float lb = __shfl_xor(l[j], off);
-      float accb[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[j][e], off);
-      merge_state(m[j], l[j], acc[j], mb, lb, accb);
-    }
-    if (sub == 0) {
-      const size_t slot = (bh0 + j) * n_splits + split;
-      float4 *dst = reinterpret_cast<float4 *>(part_acc + slot * kHeadDim + slice * 8);
-      dst[0] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
-      dst[1] = make_float4(acc[j][4], acc[j][5], acc[j][6], acc[j][7]);
-      if (slice == 0) *reinterpret_cast<float2 *>(part_ml + slot * 2) = make_float2(m[j], l[j]);
-    }
+    for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[e], off);
+    merge_state(m, l, acc, mb, lb, accb);
+  }
+
+  if (sub == 0) {
+    const size_t slot = static_cast<size_t>(bh) * n_splits + split;
+    float4 *dst = reinterpret_cast<float4 *>(part_acc + slot * kHeadDim + slice * 8);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    if (slice == 0) *reinterpret_cast<float2 *>(part_ml + slot * 2) = make_float2(m, l);
   }
 }
 
@@ -374,16 +349,262 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   }
 }
 
-// Whole-sequence variant for batches with at least one unit per compute
-// unit: one block of 8 waves owns one unit (a (b, h), or with grouped queries
-// NQ query heads of one (b, K/V head)), and wave w folds the chunks
-// w, w + 8, w + 16, ... of `chunk` rows each. Rows go in sub-steps of 32 (16
-// for NQ >= 7), the next one in flight while the current one is consumed; the
-// 8 wave states merge through LDS and the block writes the NQ outputs, so
-// there is no partial workspace and no merge pass.
+// Grouped-query split pass on the matrix cores (H_kv < H): one wave owns the
+// cache rows [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one
+// (b, K/V head) and up to 32 of the query heads that read it, and writes one
+// partial (m, l, acc[64]) per query head in the layout of the VALU split pass
+// above, so the same merge pass combines them. Per 32-row tile:
+//   S^T = K Q^T   4 x v_mfma_f32_32x32x16_f16, the group's queries as the 32
+//                 columns (columns past the group compute zeros, unused);
+//   softmax       per lane: one query column, 16 of the 32 rows (the other 16
+//                 in lane l ^ 32), log2 domain, rows past the chunk -> -inf;
+//   O^T += V^T P^T with P split into fp16 hi + lo parts (4 + 4 MFMAs), so the
+//                 weights keep fp32 accuracy whatever the number of rows.
+// K and V tiles stream through a per-wave LDS ring filled by direct
+// global->LDS loads kGroupAhead tiles ahead (row-major, 16-byte chunks
+// XOR-swizzled, as the prefill kernel's tiles). A block is one wave, so
+// nothing is shared and there is no barrier; the ring sets 5 waves per CU.
+// The MFMA work per row is the same for 1 to 32 queries, so a K/V head is
+// read once for its whole group at HBM speed, where the VALU path above pays
+// the dot products and the P V update once per query.
+constexpr int kGroupTile = 32;                           // cache rows per tile
+constexpr int kGroupStages = 4;                          // ring depth per wave (2..4)
+constexpr int kGroupAhead = kGroupStages - 1;            // tiles in flight
+constexpr int kGroupTileHalves = kGroupTile * kHeadDim;  // 4 KiB
+constexpr int kGroupLoads = 2 * kGroupTile / 8;          // K + V loads per lane per tile
+constexpr int kGroupCols = 32;                           // queries per wave
+
+constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
+
+// Online softmax and O^T += V^T P^T for one tile whose S^T (raw q.k) is in
+// `sacc`: m is the running max in the log2 domain (scores times c), l this
+// lane's share of the row sum. MASK: rows >= lim of this lane's half are past
+// the chunk end. SPLIT: P as fp16 hi + lo (two PV products) instead of one
+// fp16 rounding; l sums the same fp16 values the products consume.
+template <bool MASK, bool SPLIT>
+__device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&vf)[2][2],
+                                                 int lim, float c, float &m, float &l,
+                                                 floatx16 (&o)[2]) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int a = 0; a < 16; ++a) {
+    if (MASK && 8 * (a >> 2) + (a & 3) >= lim) sacc[a] = -INFINITY;
+    mx = fmaxf(mx, sacc[a]);
+  }
+  mx = max_lane_pair(mx);  // the tile has a row in range: finite
+  const float m_new = fmaxf(m, mx * c);
+  const float alpha = fast_exp2(m - m_new);
+  m = m_new;
+  const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  half8 p_hi[2], p_lo[2];
+  float lsum = 0.f;
+#pragma unroll
+  for (int hs = 0; hs < 2; ++hs)
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float s0 = sacc[8 * hs + e], s1 = sacc[8 * hs + e + 1];
+      float p0 = fast_exp2(fmaf(s0, c, -m_new));
+      float p1 = fast_exp2(fmaf(s1, c, -m_new));
+      if (MASK) {  // -inf * c is NaN when c = 0
+        p0 = (s0 == -INFINITY) ? 0.f : p0;
+        p1 = (s1 == -INFINITY) ? 0.f : p1;
+      }
+      const half2 hi2 = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
+      p_hi[hs][e] = hi2[0];
+      p_hi[hs][e + 1] = hi2[1];
+      lsum = __builtin_amdgcn_fdot2(hi2, ones, lsum, false);
+      if (SPLIT) {
+        const half2 lo2 = {static_cast<_Float16>(p0 - static_cast<float>(hi2[0])),
+                           static_cast<_Float16>(p1 - static_cast<float>(hi2[1]))};
+        p_lo[hs][e] = lo2[0];
+        p_lo[hs][e + 1] = lo2[1];
+        lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
+      }
+    }
+  l = fmaf(l, alpha, lsum);
+  // alpha is exactly 1 wherever the max did not rise (wave-uniform branch).
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) o[db][a] *= alpha;
+  }
+#pragma unroll
+  for (int hs = 0; hs < 2; ++hs)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      o[db] = mfma(vf[hs][db], p_hi[hs], o[db]);
+      if (SPLIT) o[db] = mfma(vf[hs][db], p_lo[hs], o[db]);
+    }
+}
+
+__global__ __launch_bounds__(kWave) void decode_group_kernel(
+    const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
+    const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
+    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads, int kv_heads,
+    int group, int nq, int max_seq, int n_splits, int n_units, int chunk, float qscale) {
+  __shared__ __attribute__((aligned(1024))) _Float16 lds[2 * kGroupStages * kGroupTileHalves];
+  const int unit = static_cast<int>(blockIdx.x);
+  if (unit >= n_units) return;
+  const int lane = threadIdx.x;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  // Chunk-major unit order, as the VALU split pass (longest-first dispatch).
+  const int n_qu = n_units / n_splits;
+  const int split = unit / n_qu;
+  const QueryUnit qu = query_unit(unit - split * n_qu, kv_heads, group / nq, group, nq);
+  const int len = min(seq_lens[qu.b], max_seq);
+  const int begin = split * chunk;
+  if (begin >= len) return;  // no rows: no partial (the merge skips this chunk)
+  const int end = min(len, begin + chunk);
+  const int n_tiles = (end - begin + kGroupTile - 1) / kGroupTile;
+
+  const size_t kv_off = (static_cast<size_t>(qu.b) * kv_heads + qu.kv) * max_seq * kHeadDim;
+  const _Float16 *const kp = k_cache + kv_off;
+  const _Float16 *const vp = v_cache + kv_off;
+  _Float16 *const kring = lds;
+  _Float16 *const vring = lds + kGroupStages * kGroupTileHalves;
+
+  // Loads of tile t: lane = 8 * (row in an 8-row block) + 16-byte chunk; four
+  // row blocks each of K and V. Rows past the chunk end are clamped to its
+  // last row (they are masked out of the softmax).
+  const int r8 = lane >> 3;
+  const int c16 = lane & 7;
+  int src_k[4], src_v[4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int r = rb * 8 + r8;  // row inside the tile (tile rows start at a multiple of 32)
+    src_k[rb] = (c16 ^ k_swz(r)) << 3;
+    src_v[rb] = (c16 ^ v_swz(r)) << 3;
+  }
+  auto issue = [&](int t) {
+    const int row0 = begin + t * kGroupTile;
+    _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
+    _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const size_t row = static_cast<size_t>(min(row0 + rb * 8 + r8, end - 1)) * kHeadDim;
+      global_to_lds16(kp + row + src_k[rb], ks + rb * 8 * kHeadDim);
+      global_to_lds16(vp + row + src_v[rb], vs + rb * 8 * kHeadDim);
+    }
+  };
+  // Q^T fragments: column `col` is query head h0 + col of the unit (zeros
+  // past nq), head dims [32 g + 8 s, +8) for k-step s. They are waited for
+  // here, before the ring's first loads: a Q load still pending inside the
+  // loop would make the compiler wait for every load (ring included) there.
+  half8 qf[4];
+  const size_t bh0 = static_cast<size_t>(qu.b) * heads + qu.h0;
+  const int qcol = min(col, nq - 1);  // columns past nq load a valid row, then zero it
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    qf[st] = *reinterpret_cast<const half8 *>(q + (bh0 + qcol) * kHeadDim + 32 * g + 8 * st);
+  // A negative scale is folded into Q (an exact fp16 negation), so the
+  // softmax works with c = |scale| log2(e) > 0 and takes its max on the raw
+  // scores.
+  const float c_scale = fabsf(qscale);
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    if (col >= nq) qf[st] = half8{};
+    if (qscale < 0.f) qf[st] = -qf[st];
+    asm volatile("" ::"v"(qf[st]));
+  }
+
+#pragma unroll
+  for (int t = 0; t < kGroupAhead; ++t)
+    if (t < n_tiles) issue(t);
+
+  const FragOffsets fo = frag_offsets(lane);
+  float m = kNegBig, l = 0.f;
+  floatx16 o[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) o[db][a] = 0.f;
+
+  // The last tile is partial when the chunk's row count is not a multiple of
+  // 32: only that tile is masked. Sequences shorter than kGroupSplitPBelow
+  // rows get the split (hi + lo) P product on every tile.
+  const bool partial_tail = ((end - begin) & (kGroupTile - 1)) != 0;
+  auto run = [&](auto split_tag) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
+    for (int t = 0; t < n_tiles; ++t) {
+      // Tile t resident: the loads of the tiles issued after it (up to
+      // kGroupAhead - 1 of them) may still fly.
+      const int later = min(kGroupAhead - 1, n_tiles - 1 - t);
+      if (kGroupAhead > 2 && later >= 2)
+        wait_loads<(kGroupAhead > 2 ? 2 : 0) * kGroupLoads>();
+      else if (kGroupAhead > 1 && later == 1)
+        wait_loads<(kGroupAhead > 1 ? 1 : 0) * kGroupLoads>();
+      else
+        wait_loads<0>();
+      const _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
+      const _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
+      half8 kf[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) kf[st] = *reinterpret_cast<const half8 *>(ks + fo.k[st]);
+      half8 vf[2][2];  // [16-row step][d-block]
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        lds_half *pv = opaque_lds(vs + fo.v[db]);
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs)
+#pragma unroll
+          for (int part = 0; part < 2; ++part) {
+            const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v *)(pv + (16 * hs + 8 * part) * kHeadDim));
+            const half4 v4 = __builtin_bit_cast(half4, r);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vf[hs][db][4 * part + e] = v4[e];
+          }
+      }
+      // The stage of tile t - 1 is free (its fragments were consumed): refill
+      // it with tile t + kGroupAhead.
+      if (t + kGroupAhead < n_tiles) issue(t + kGroupAhead);
+
+      floatx16 sacc;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) sacc = mfma(kf[st], qf[st], sacc);
+      if (partial_tail && t == n_tiles - 1) {
+        // Element a: row 8 (a / 4) + 4 g + a % 4 of the tile.
+        const int lim = end - (begin + t * kGroupTile) - 4 * g;
+        group_softmax_pv<true, SPLIT>(sacc, vf, lim, c_scale, m, l, o);
+      } else {
+        group_softmax_pv<false, SPLIT>(sacc, vf, 0, c_scale, m, l, o);
+      }
+    }
+  };
+  if (len < kGroupSplitPBelow)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+
+  // Lanes l and l ^ 32 hold the two row halves of column col: m is shared,
+  // l adds up; each lane writes its 32 of the 64 head dims.
+  l += __shfl_xor(l, 32);
+  if (col < nq) {
+    const size_t slot = (bh0 + col) * n_splits + split;
+    float *const dst = part_acc + slot * kHeadDim;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+        *reinterpret_cast<float4 *>(dst + db * 32 + 8 * rb + 4 * g) =
+            make_float4(o[db][4 * rb], o[db][4 * rb + 1], o[db][4 * rb + 2], o[db][4 * rb + 3]);
+    if (g == 0) *reinterpret_cast<float2 *>(part_ml + slot * 2) = make_float2(m, l);
+  }
+}
+
+// Whole-sequence variant for batches with at least one (b, h) per compute
+// unit: one block of 8 waves owns one (b, h), and wave w folds the chunks
+// w, w + 8, w + 16, ... of `chunk` rows each. Rows go in sub-steps of 32, the
+// next one in flight while the current one is consumed; the 8 wave states
+// merge through LDS and the block writes the output, so there is no partial
+// workspace and no merge pass.
 // With chunk == 0 (the automatic choice) the chunk follows the grid:
 //  * every block resident at once (target_waves > 0): the batch's cache rows
-//    times the blocks per batch row, over target_waves, so about target_waves waves stream rows, each a long
+//    over target_waves, so about target_waves waves stream rows, each a long
 //    contiguous range (measured on ragged batches: fewer, longer streams beat
 //    more, shorter ones);
 //  * more blocks than fit (target_waves == 0): 1/8 of the block's own
@@ -393,37 +614,30 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 // up to kRankMax), so the dispatcher runs a longest-first list schedule.
 constexpr int kBhWaves = 8;
 constexpr int kBhThreads = kBhWaves * kWave;
-// Row groups per sub-step: 4 (32 rows), 2 for 7-8 queries per block, whose
-// per-query state would otherwise not fit in 256 VGPRs.
-template <int NQ>
-constexpr int bh_groups() {
-  return NQ <= 6 ? 4 : 2;
-}
+constexpr int kBhGroups = 4;  // 32-row sub-steps
 constexpr int kRankMax = 256;   // ranking costs batch^2 / 512 LDS reads per thread
 constexpr int kBhWavesPerCu = 5;  // streaming waves per CU when the grid is resident
 
-template <int NQ, bool OUT_F32>
+template <bool OUT_F32>
 __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
-    void *__restrict__ o, int batch, int heads, int kv_heads, int group, int max_seq,
-    int chunk, int target_waves, float qscale) {
+    void *__restrict__ o, int batch, int heads, int max_seq, int chunk,
+    int target_waves, float qscale) {
   __shared__ int s_len[kRankMax];
   __shared__ int s_order[kRankMax];
-  __shared__ float s_acc[kBhWaves][NQ][kHeadDim];
-  __shared__ float s_m[kBhWaves][NQ];
-  __shared__ float s_l[kBhWaves][NQ];
+  __shared__ float s_acc[kBhWaves][kHeadDim];
+  __shared__ float s_m[kBhWaves];
+  __shared__ float s_l[kBhWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  // Blocks per batch row: one per (kv head, query chunk).
-  const int q_chunks = group / NQ;
-  const int per_b = kv_heads * q_chunks;
-  QueryUnit qu = query_unit(static_cast<int>(blockIdx.x), kv_heads, q_chunks, group, NQ);
+  int b = static_cast<int>(blockIdx.x) / heads;
+  const int h = static_cast<int>(blockIdx.x) % heads;
   if (batch <= kRankMax) {
-    // rank(t) = #{u : len_u > len_t or (len_u == len_t and u < t)}: the
-    // blocks of batch slot i take the i-th longest sequence.
+    // rank(t) = #{u : len_u > len_t or (len_u == len_t and u < t)}: block i
+    // takes the (i / H)-th longest sequence.
     for (int t = tid; t < batch; t += kBhThreads) s_len[t] = max(0, min(seq_lens[t], max_seq));
     __syncthreads();
     for (int t = tid; t < batch; t += kBhThreads) {
@@ -436,9 +650,9 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
       s_order[rank] = t;
     }
     __syncthreads();
-    qu.b = s_order[qu.b];
+    b = s_order[b];
   }
-  const int b = qu.b;
+  const int bh = b * heads + h;
   const int len = max(0, min(seq_lens[b], max_seq));
   if (chunk == 0) {
     int rows_per_wave;
@@ -450,7 +664,7 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
       for (int off = kWave / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
       const float total = static_cast<float>(__builtin_amdgcn_readfirstlane(part));
       rows_per_wave = static_cast<int>(
-          fminf(ceilf(total * static_cast<float>(per_b) / static_cast<float>(target_waves)),
+          fminf(ceilf(total * static_cast<float>(heads) / static_cast<float>(target_waves)),
                 static_cast<float>(max_seq)));
     } else {
       rows_per_wave = (len + kBhWaves - 1) / kBhWaves;
@@ -461,30 +675,23 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
 
   const int sub = lane >> 3;   // row inside an 8-row group
   const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
-  const size_t kv_off = (static_cast<size_t>(b) * kv_heads + qu.kv) * max_seq * kHeadDim;
-  const _Float16 *kp = k_cache + kv_off;
-  const _Float16 *vp = v_cache + kv_off;
-  const size_t bh0 = static_cast<size_t>(b) * heads + qu.h0;
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const _Float16 *kp = k_cache + head_off;
+  const _Float16 *vp = v_cache + head_off;
 
-  float m[NQ], l[NQ], acc[NQ][8];
+  float m = kNegBig, l = 0.f, acc[8];
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    m[j] = kNegBig;
-    l[j] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  }
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
-  constexpr int kGroups = bh_groups<NQ>();
-  constexpr int kStepRows = kRowsPerGroup * kGroups;
+  constexpr int kStepRows = kRowsPerGroup * kBhGroups;  // 32
   const int stride = kBhWaves * chunk;  // distance between a wave's chunks
   int c0 = wave * chunk;                // this wave's current chunk
   if (c0 < len) {
-    half2 qh[NQ][4];
-    load_queries<NQ>(q, bh0, slice, qh);
+    half2 qh[4];
+    load_query(q, bh, slice, qh);
     int end = min(len, c0 + chunk);
     int row0 = c0;
-    RowSlotsT<kGroups> cur, nxt;
+    RowSlotsT<kBhGroups> cur, nxt;
     load_slots(cur, kp, vp, row0, end, sub, slice);
     for (;;) {
       // Next sub-step: the rest of this chunk, else this wave's next chunk.
@@ -505,44 +712,39 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     }
   }
 
+  // Merge the 8 row groups of the wave (lanes that share `slice`).
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    // Merge the 8 row groups of the wave (lanes that share `slice`).
+  for (int off = 8; off < kWave; off <<= 1) {
+    const float mb = __shfl_xor(m, off);
+    const float lb = __shfl_xor(l, off);
+    float accb[8];
 #pragma unroll
-    for (int off = 8; off < kWave; off <<= 1) {
-      const float mb = __shfl_xor(m[j], off);
-      const float lb = __shfl_xor(l[j], off);
-      float accb[8];
+    for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[e], off);
+    merge_state(m, l, acc, mb, lb, accb);
+  }
+  if (sub == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[j][e], off);
-      merge_state(m[j], l[j], acc[j], mb, lb, accb);
-    }
-    if (sub == 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][j][slice * 8 + e] = acc[j][e];
-      if (slice == 0) {
-        s_m[wave][j] = m[j];
-        s_l[wave][j] = l[j];
-      }
+    for (int e = 0; e < 8; ++e) s_acc[wave][slice * 8 + e] = acc[e];
+    if (slice == 0) {
+      s_m[wave] = m;
+      s_l[wave] = l;
     }
   }
   __syncthreads();
-  if (tid < NQ * kHeadDim) {  // NQ <= 8: one thread per (query, head dim)
-    const int j = tid / kHeadDim;
-    const int d = tid % kHeadDim;
-    float mb = s_m[0][j];
+  if (tid < kHeadDim) {
+    float mb = s_m[0];
 #pragma unroll
-    for (int w = 1; w < kBhWaves; ++w) mb = fmaxf(mb, s_m[w][j]);
+    for (int w = 1; w < kBhWaves; ++w) mb = fmaxf(mb, s_m[w]);
     float lb = 0.f, ab = 0.f;
 #pragma unroll
     for (int w = 0; w < kBhWaves; ++w) {
-      const float f = fast_exp2(s_m[w][j] - mb);  // empty waves: l = 0, acc = 0
-      lb = fmaf(s_l[w][j], f, lb);
-      ab = fmaf(s_acc[w][j][d], f, ab);
+      const float f = fast_exp2(s_m[w] - mb);  // empty waves: l = 0, acc = 0
+      lb = fmaf(s_l[w], f, lb);
+      ab = fmaf(s_acc[w][tid], f, ab);
     }
     // decode.cu:172: a sequence with no rows gets a zero output.
     const float out = (lb > 0.f) ? ab / lb : 0.f;
-    const size_t idx = (bh0 + j) * kHeadDim + d;
+    const size_t idx = static_cast<size_t>(bh) * kHeadDim + tid;
     if (OUT_F32)
       static_cast<float *>(o)[idx] = out;
     else
@@ -550,74 +752,66 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   }
 }
 
-// Queries per unit for a query group of `group` heads per K/V head: the
-// largest divisor of the group up to kMaxGroupQueries, so every unit holds
-// the same number of queries and a group of up to 8 reads its K/V head once.
-constexpr int kMaxGroupQueries = 8;
-int queries_per_unit(int group) {
-  for (int nq = kMaxGroupQueries; nq > 1; --nq)
+// Blocks of decode_bh_kernel resident on one CU at once, per device.
+int bh_blocks_per_cu(int device) {
+  static std::once_flag once[kMaxDevices];
+  static int blocks[kMaxDevices];
+  if (device < 0 || device >= kMaxDevices) return 1;
+  std::call_once(once[device], [device] {
+    int n = 0;
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    if (hipSetDevice(device) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void *>(decode_bh_kernel<false>), kBhThreads, 0) !=
+            hipSuccess)
+      n = 0;
+    (void)hipSetDevice(prev);
+    blocks[device] = n;
+  });
+  return blocks[device] > 0 ? blocks[device] : 1;
+}
+
+// Whole-sequence blocks need at least one (b, h) per compute unit to fill
+// the chip; below that, the split-K grid spreads each sequence over CUs.
+bool use_bh_path(int batch, int heads) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const int cu = device_cu_count(dev);
+  return cu > 0 && static_cast<long long>(batch) * heads >= cu;
+}
+
+// Queries per wave of the grouped pass: the largest divisor of the group
+// that fits the 32 columns of one MFMA tile.
+int group_queries(int group) {
+  for (int nq = min(group, kGroupCols); nq > 1; --nq)
     if (group % nq == 0) return nq;
   return 1;
 }
 
-// Calls f(std::integral_constant<int, NQ>) for the runtime nq in [1, 8].
-template <typename F>
-void with_nq(int nq, F &&f) {
-  switch (nq) {
-    case 1: f(std::integral_constant<int, 1>{}); break;
-    case 2: f(std::integral_constant<int, 2>{}); break;
-    case 3: f(std::integral_constant<int, 3>{}); break;
-    case 4: f(std::integral_constant<int, 4>{}); break;
-    case 5: f(std::integral_constant<int, 5>{}); break;
-    case 6: f(std::integral_constant<int, 6>{}); break;
-    case 7: f(std::integral_constant<int, 7>{}); break;
-    default: f(std::integral_constant<int, 8>{}); break;
-  }
-}
-
-// Row groups per sub-step of the split kernel: 8 for one query per unit,
-// 4 for grouped queries (their per-query state takes the registers).
-template <int NQ>
-constexpr int split_groups() {
-  return NQ == 1 ? kGroupsPerStep : kGroupsPerStep / 2;
-}
-
-// Blocks of decode_bh_kernel<nq> resident on one CU at once, per device.
-int bh_blocks_per_cu(int device, int nq) {
-  static std::once_flag once[kMaxDevices][kMaxGroupQueries];
-  static int blocks[kMaxDevices][kMaxGroupQueries];
-  if (device < 0 || device >= kMaxDevices || nq < 1 || nq > kMaxGroupQueries) return 1;
-  std::call_once(once[device][nq - 1], [device, nq] {
-    int n = 0;
-    int prev = 0;
-    if (hipGetDevice(&prev) != hipSuccess) return;
-    const void *fn = nullptr;
-    with_nq(nq, [&fn](auto c) {
-      fn = reinterpret_cast<const void *>(decode_bh_kernel<decltype(c)::value, false>);
-    });
-    if (hipSetDevice(device) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kBhThreads, 0) != hipSuccess)
-      n = 0;
-    (void)hipSetDevice(prev);
-    blocks[device][nq - 1] = n;
-  });
-  return blocks[device][nq - 1] > 0 ? blocks[device][nq - 1] : 1;
-}
-
-// Whole-sequence blocks need at least one unit per compute unit to fill the
-// chip; below that, the split-K grid spreads each sequence over CUs.
-bool use_bh_path(int batch, int units_per_row) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
-  const int cu = device_cu_count(dev);
-  return cu > 0 && static_cast<long long>(batch) * units_per_row >= cu;
-}
+// Waves of decode_group_kernel the automatic chunk aims at: the 5 per CU its
+// LDS ring lets run at once.
+constexpr int kGroupWavesPerCu = 5;
 
 }  // namespace
 
 int decode_units_per_row(int heads, int kv_heads) {
   const int group = heads / kv_heads;
-  return kv_heads * (group / queries_per_unit(group));
+  if (group == 1) return heads;
+  return kv_heads * (group / group_queries(group));
+}
+
+int decode_group_chunk(int batch, int units_per_row, int max_seq) {
+  int dev = 0;
+  int cu = 0;
+  if (hipGetDevice(&dev) == hipSuccess) cu = device_cu_count(dev);
+  const long long waves = static_cast<long long>(kGroupWavesPerCu) * (cu > 0 ? cu : 256);
+  const long long work = static_cast<long long>(max_seq) * batch * units_per_row;
+  long long rows = (work + waves - 1) / waves;
+  rows = ((rows + kGroupTile - 1) / kGroupTile) * kGroupTile;
+  const long long cap = ((static_cast<long long>(max_seq) + kGroupTile - 1) / kGroupTile) * kGroupTile;
+  rows = std::max<long long>(rows, 2 * kGroupTile);
+  return static_cast<int>(std::min(rows, std::max<long long>(cap, 2 * kGroupTile)));
 }
 
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
@@ -625,49 +819,69 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   int heads, int kv_heads, int max_seq, float scale, int split_size,
                   bool auto_split, float *workspace, hipStream_t stream) {
   const int group = heads / kv_heads;
-  const int nq = queries_per_unit(group);
-  const int units_per_row = kv_heads * (group / nq);
-  const size_t n_qu = static_cast<size_t>(batch) * units_per_row;
+  if (group > 1) {
+    // Grouped queries: the matrix-core split pass, then the common merge.
+    const int nqg = group_queries(group);
+    const size_t n_qg = static_cast<size_t>(batch) * kv_heads * (group / nqg);
+    const int n_sp = (max_seq + split_size - 1) / split_size;
+    const size_t n_gu = n_qg * n_sp;
+    float *part_acc = workspace;
+    float *part_ml = workspace + static_cast<size_t>(batch) * heads * n_sp * kHeadDim;
+    hipLaunchKernelGGL(decode_group_kernel, dim3(static_cast<unsigned>(n_gu)), dim3(kWave), 0,
+                       stream, static_cast<const _Float16 *>(q),
+                       static_cast<const _Float16 *>(k_cache),
+                       static_cast<const _Float16 *>(v_cache), seq_lens, part_acc, part_ml,
+                       heads, kv_heads, group, nqg, max_seq, n_sp, static_cast<int>(n_gu),
+                       split_size, scale * kLog2e);
+    int rc = check_hip(hipGetLastError(), "decode_group_kernel launch");
+    if (rc != FA_OK) return rc;
+    const unsigned n_bh = static_cast<unsigned>(static_cast<size_t>(batch) * heads);
+    if (out_f32)
+      hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(n_bh), dim3(kMergeThreads), 0, stream,
+                         part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
+    else
+      hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(n_bh), dim3(kMergeThreads), 0, stream,
+                         part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
+    return check_hip(hipGetLastError(), "decode_merge_kernel launch");
+  }
+  const int n_splits = (max_seq + split_size - 1) / split_size;
   const size_t bh = static_cast<size_t>(batch) * heads;
-  const float qscale = scale * kLog2e;
-  const auto *qh = static_cast<const _Float16 *>(q);
-  const auto *kh = static_cast<const _Float16 *>(k_cache);
-  const auto *vh = static_cast<const _Float16 *>(v_cache);
-  if (use_bh_path(batch, units_per_row)) {
+  if (use_bh_path(batch, heads)) {
     int dev = 0;
     int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
     if (rc != FA_OK) return rc;
     const int cu = device_cu_count(dev);
-    const bool resident = n_qu <= static_cast<size_t>(bh_blocks_per_cu(dev, nq)) * cu;
+    const bool resident = bh <= static_cast<size_t>(bh_blocks_per_cu(dev)) * cu;
     const int target_waves = resident ? kBhWavesPerCu * cu : 0;
-    const int chunk = auto_split ? 0 : split_size;
-    with_nq(nq, [&](auto c) {
-      constexpr int NQ = decltype(c)::value;
-      if (out_f32)
-        hipLaunchKernelGGL((decode_bh_kernel<NQ, true>), dim3(static_cast<unsigned>(n_qu)),
-                           dim3(kBhThreads), 0, stream, qh, kh, vh, seq_lens, o, batch, heads,
-                           kv_heads, group, max_seq, chunk, target_waves, qscale);
-      else
-        hipLaunchKernelGGL((decode_bh_kernel<NQ, false>), dim3(static_cast<unsigned>(n_qu)),
-                           dim3(kBhThreads), 0, stream, qh, kh, vh, seq_lens, o, batch, heads,
-                           kv_heads, group, max_seq, chunk, target_waves, qscale);
-    });
+    if (out_f32)
+      hipLaunchKernelGGL(decode_bh_kernel<true>, dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
+    else
+      hipLaunchKernelGGL(decode_bh_kernel<false>, dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
     return check_hip(hipGetLastError(), "decode_bh_kernel launch");
   }
-  const int n_splits = (max_seq + split_size - 1) / split_size;
   float *part_acc = workspace;
   float *part_ml = workspace + bh * n_splits * kHeadDim;
-  const size_t n_units = n_qu * n_splits;
+  const size_t n_units = bh * n_splits;
   const unsigned split_blocks =
       static_cast<unsigned>((n_units + kSplitWaves - 1) / kSplitWaves);
 
-  with_nq(nq, [&](auto c) {
-    constexpr int NQ = decltype(c)::value;
-    hipLaunchKernelGGL((decode_split_kernel<split_groups<NQ>(), NQ>), dim3(split_blocks),
-                       dim3(kSplitThreads), 0, stream, qh, kh, vh, seq_lens, part_acc, part_ml,
-                       heads, kv_heads, group, max_seq, n_splits, static_cast<int>(n_units),
-                       split_size, qscale);
-  });
+  hipLaunchKernelGGL(decode_split_kernel, dim3(split_blocks),
+                     dim3(kSplitThreads), 0, stream,
+                     static_cast<const _Float16 *>(q),
+                     static_cast<const _Float16 *>(k_cache),
+                     static_cast<const _Float16 *>(v_cache), seq_lens,
+                     part_acc, part_ml, heads, max_seq, n_splits,
+                     static_cast<int>(n_units), split_size, scale * kLog2e);
   int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
   if (rc != FA_OK) return rc;
 
@@ -686,12 +900,13 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
 int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
   struct K { const char *name; const void *fn; int threads; };
   const K ks[] = {
-      {"decode_split_kernel",
-       reinterpret_cast<const void *>(decode_split_kernel<kGroupsPerStep, 1>), kSplitThreads},
+      {"decode_split_kernel", reinterpret_cast<const void *>(decode_split_kernel),
+       kSplitThreads},
       {"decode_merge_kernel",
        reinterpret_cast<const void *>(decode_merge_kernel<false>), kMergeThreads},
-      {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<1, false>),
+      {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<false>),
        kBhThreads},
+      {"decode_group_kernel", reinterpret_cast<const void *>(decode_group_kernel), kWave},
   };
   for (const K &k : ks) {
     if (*n < cap) {

@@ -44,9 +44,13 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int kv_heads, int max_seq, float scale, int split_size,
                   bool auto_split, float *workspace, hipStream_t stream);
-// Decode work units per batch row (one per K/V head and query chunk; one
-// per head without grouped queries): the split chooser's "heads".
+// Decode work units per batch row: one per head without grouped queries,
+// else one per (K/V head, chunk of up to 32 of its query heads).
 int decode_units_per_row(int heads, int kv_heads);
+// Automatic chunk (cache rows per split) of the grouped-query decode pass:
+// the batch's max_seq-row work over the waves the GPU runs at once, in
+// multiples of 32 rows, at least 64.
+int decode_group_chunk(int batch, int units_per_row, int max_seq);
 
 // Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);

@@ -1,0 +1,131 @@
+// MFMA tile building blocks shared by the gfx950 attention kernels
+// (prefill.hip, decode.hip): the 16-byte-chunk swizzles of a row-major
+// [rows x 64] fp16 tile in LDS, direct global->LDS loads, the fragment
+// offsets of v_mfma_f32_32x32x16_f16 operands read from such a tile, and the
+// lane-pair max of an S^T accumulator.
+//
+// Operand conventions (lane l: column l % 32, half g = l / 32):
+//   S^T = K Q^T : A = 32 key rows x 16 head dims, B = 16 head dims x 32
+//                 queries; the 64 head dims are grouped [32 g + 8 s, +8) for
+//                 k-step s, so every fragment is one 16-byte chunk of a row.
+//   O^T += V^T P^T : A = V^T read from a row-major V tile with
+//                 ds_read_b64_tr_b16; B = P^T taken from the S^T
+//                 accumulators in their own key order.
+// Accumulator element a of a 32 x 32 tile sits at row 8 (a / 4) + 4 g + a % 4
+// of column l % 32.
+#pragma once
+
+#include "fa_internal.h"
+
+namespace fa {
+namespace {
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Chunk swizzles (16-byte chunk index within a 128-byte row).
+//  K, Q: a ds_read_b128 phase reads the same logical chunk of 8 (32 banks) or
+//     16 (64 banks) consecutive rows; f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2)
+//     is a bijection on every 8 consecutive rows and keeps the 8 even and the
+//     8 odd rows of any 16 apart, so both bank layouts are conflict free.
+//  V: a 16-lane transpose-read phase reads chunks {c, c+1} (c even) of 4
+//     consecutive rows: c ^ 2 (row & 3) puts them in 8 distinct bank groups.
+__device__ __forceinline__ int k_swz(int row) {
+  return ((row >> 1) & 7) ^ ((row & 1) << 2);
+}
+__device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
+
+// One direct global->LDS load: 16 bytes per lane from `src` to LDS address
+// m0 + 16 * lane. Written in asm so the compiler does not treat later LDS
+// reads of other stages as possibly aliasing the in-flight write (it would
+// otherwise wait for every outstanding load before each of them); the ring
+// tracks completion itself with explicit vmcnt waits.
+// m0 is listed as clobbered for the reader; the compiler treats m0 as a
+// reserved register and does not track it (hence the silenced warning), which
+// is safe because nothing else in the kernels that use it reads m0 (checked in
+// the generated ISA: every m0 write is the one in this function).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void global_to_lds16(const void *src, const void *lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(lds_dst))));
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(m0)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N of this thread's global->LDS loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  if constexpr (N == 0)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
+                                         const floatx16 &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Per-lane LDS offsets (in halves, relative to a tile) of every fragment a
+// wave reads from a tile; loop invariant.
+struct FragOffsets {
+  int k[4];  // K (and Q) fragment for d-step s (32-key block 0; block 1 is +32 rows)
+  int v[2];  // V^T transpose-read base for d-block db (key sub-blocks add rows)
+};
+
+__device__ __forceinline__ FragOffsets frag_offsets(int lane) {
+  FragOffsets f;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    f.k[s] = col * kHeadDim + (((4 * g + s) ^ k_swz(col)) << 3);
+  // Lane l of a 16-lane group points at row 4 g + (l % 16) / 4 (plus the
+  // 8-key sub-block), head dims [16 ((l / 16) % 2) + 4 (l % 4), +4).
+  const int tr_row = 4 * g + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+  for (int db = 0; db < 2; ++db) {
+    const int d = db * 32 + tr_dim;
+    f.v[db] = tr_row * kHeadDim + (((d >> 3) ^ v_swz(tr_row)) << 3) + (d & 7);
+  }
+  return f;
+}
+
+typedef __attribute__((address_space(3))) const _Float16 lds_half;
+
+// An LDS address the compiler must materialise as one register per step:
+// the constant row offsets of the reads below then fold into the
+// instructions' offset fields instead of being hoisted out of the loop as
+// separate loop-invariant addresses.
+__device__ __forceinline__ lds_half *opaque_lds(const _Float16 *p) {
+  unsigned a = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p)));
+  asm volatile("" : "+v"(a));
+  return reinterpret_cast<lds_half *>(static_cast<uintptr_t>(a));
+}
+
+// max(x[l], x[l ^ 32]) for every lane: one v_permlane32_swap (VALU), no LDS.
+// With both operands holding x, the swap leaves lanes 0-31 of the first
+// register and lanes 32-63 of the second unchanged and exchanges the other
+// halves, so the two registers hold x[l] and x[l ^ 32] in some order. It is
+// written in asm: the compiler treats a swap of two equal values as a no-op
+// and folds the max away.
+__device__ __forceinline__ float max_lane_pair(float x) {
+  float a = x, b = x;
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "s_nop 0\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
+}
+
+}  // namespace
+}  // namespace fa

@@ -76,6 +76,7 @@
 // at >= 256 keys, 1.2e-4 at >= 128 keys).
 
 #include "fa_internal.h"
+#include "mfma_tile.h"
 
 namespace fa {
 namespace {
@@ -99,60 +100,9 @@ constexpr int kQHalves = kBr * kHeadDim;                         // 16 KiB
 constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
 constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 KiB
 
-typedef short short4v __attribute__((ext_vector_type(4)));
-
-// Chunk swizzles (16-byte chunk index within a 128-byte row).
-//  K, Q: a ds_read_b128 phase reads the same logical chunk of 8 (32 banks) or
-//     16 (64 banks) consecutive rows; f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2)
-//     is a bijection on every 8 consecutive rows and keeps the 8 even and the
-//     8 odd rows of any 16 apart, so both bank layouts are conflict free.
-//  V: a 16-lane transpose-read phase reads chunks {c, c+1} (c even) of 4
-//     consecutive rows: c ^ 2 (row & 3) puts them in 8 distinct bank groups.
-__device__ __forceinline__ int k_swz(int row) {
-  return ((row >> 1) & 7) ^ ((row & 1) << 2);
-}
-__device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
-
-// One direct global->LDS load: 16 bytes per lane from `src` to LDS address
-// m0 + 16 * lane. Written in asm so the compiler does not treat later LDS
-// reads of other stages as possibly aliasing the in-flight write (it would
-// otherwise wait for every outstanding load before each of them); the ring
-// tracks completion itself with explicit vmcnt waits.
-// m0 is listed as clobbered for the reader; the compiler treats m0 as a
-// reserved register and does not track it (hence the silenced warning), which
-// is safe because nothing else in this file's kernels reads m0 (checked in the
-// generated ISA: every m0 write is the one in this function).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void global_to_lds16(const void *src, const void *lds_dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(lds_dst))));
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "s"(m0)
-      : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// Wait until at most N of this thread's global->LDS loads are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_loads() {
-  if constexpr (N == 0)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
   return *reinterpret_cast<const half8 *>(p);
-}
-
-__device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
-                                         const floatx16 &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 struct SoftmaxState {
@@ -161,47 +111,10 @@ struct SoftmaxState {
   floatx16 o[2]; // O^T accumulators: d-blocks 0 and 1
 };
 
-// Per-lane LDS offsets (in halves, relative to a tile) of every fragment a
-// wave reads from a tile; loop invariant.
-struct FragOffsets {
-  int k[4];  // K (and Q) fragment for d-step s (32-key block 0; block 1 is +32 rows)
-  int v[2];  // V^T transpose-read base for d-block db (key sub-blocks add rows)
-};
-
-__device__ __forceinline__ FragOffsets frag_offsets(int lane) {
-  FragOffsets f;
-  const int col = lane & 31;
-  const int g = lane >> 5;
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    f.k[s] = col * kHeadDim + (((4 * g + s) ^ k_swz(col)) << 3);
-  // Lane l of a 16-lane group points at row 4 g + (l % 16) / 4 (plus the
-  // 8-key sub-block), head dims [16 ((l / 16) % 2) + 4 (l % 4), +4).
-  const int tr_row = 4 * g + ((lane & 15) >> 2);
-  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-  for (int db = 0; db < 2; ++db) {
-    const int d = db * 32 + tr_dim;
-    f.v[db] = tr_row * kHeadDim + (((d >> 3) ^ v_swz(tr_row)) << 3) + (d & 7);
-  }
-  return f;
-}
-
 // Register copies of the LDS fragments one tile step consumes.
 struct KFrags { half8 f[2][4]; };  // [32-key block][d-step]
 struct VFrags { half8 f[4][2]; };  // [16-key step][d-block]
 
-typedef __attribute__((address_space(3))) const _Float16 lds_half;
-
-// An LDS address the compiler must materialise as one register per step:
-// the constant row offsets of the reads below then fold into the
-// instructions' offset fields instead of being hoisted out of the loop as
-// separate loop-invariant addresses.
-__device__ __forceinline__ lds_half *opaque_lds(const _Float16 *p) {
-  unsigned a = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p)));
-  asm volatile("" : "+v"(a));
-  return reinterpret_cast<lds_half *>(static_cast<uintptr_t>(a));
-}
 
 __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
                                        const FragOffsets &fo, KFrags &k) {
@@ -255,23 +168,6 @@ __device__ __forceinline__ void pv_mfma(const VFrags &v, const half8 (&p)[4],
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int db = 0; db < 2; ++db) o[db] = mfma(v.f[ks][db], p[ks], o[db]);
-}
-
-// max(x[l], x[l ^ 32]) for every lane: one v_permlane32_swap (VALU), no LDS.
-// With both operands holding x, the swap leaves lanes 0-31 of the first
-// register and lanes 32-63 of the second unchanged and exchanges the other
-// halves, so the two registers hold x[l] and x[l ^ 32] in some order. It is
-// written in asm: the compiler treats a swap of two equal values as a no-op
-// and folds the max away.
-__device__ __forceinline__ float max_lane_pair(float x) {
-  float a = x, b = x;
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_permlane32_swap_b32 %0, %1\n\t"
-      "s_nop 0\n\t"
-      "v_max_f32 %0, %0, %1"
-      : "+v"(a), "+v"(b));
-  return a;
 }
 
 // New running max for one tile; returns alpha, the factor that rescales the

@@ -168,19 +168,25 @@ int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_d
 }
 
 // Resolves split_size 0 to the automatic choice; returns an fa_status.
-// `units` is the number of decode units per batch row.
-int resolve_split(int batch, int units, int max_seq, int *split_size) {
+// Without grouped queries that is the reference's chooser; with them, the
+// grouped pass's own chunk (it has no reference counterpart).
+int resolve_split(int batch, int heads, int kv_heads, int max_seq, int *split_size) {
   if (*split_size < 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "decode split size must be >= 0, got %d", *split_size);
   if (*split_size == 0) {
+    if (kv_heads != heads) {
+      *split_size =
+          decode_group_chunk(batch, decode_units_per_row(heads, kv_heads), max_seq);
+      return FA_OK;
+    }
     int dev = 0;
     int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
     if (rc != FA_OK) return rc;
     int min_blocks = 0;
     rc = fa_decode_min_blocks(dev, &min_blocks);
     if (rc != FA_OK) return rc;
-    *split_size = fa_choose_decode_split(max_seq, batch, units, min_blocks);
+    *split_size = fa_choose_decode_split(max_seq, batch, heads, min_blocks);
   }
   // csrc/decode.cu:209-211.
   if (*split_size % 4 != 0)
@@ -204,9 +210,7 @@ size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq,
     return 0;
   }
   if (check_groups(heads, kv_heads) != FA_OK) return 0;
-  if (resolve_split(batch, decode_units_per_row(heads, kv_heads), max_seq, &split_size) !=
-      FA_OK)
-    return 0;
+  if (resolve_split(batch, heads, kv_heads, max_seq, &split_size) != FA_OK) return 0;
   return decode_ws_bytes(batch, heads, max_seq, split_size);
 }
 
@@ -238,8 +242,7 @@ int decode_impl(const void *q, const void *k_cache, const void *v_cache,
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
   const bool auto_split = split_size == 0;
-  const int units = decode_units_per_row(heads, kv_heads);
-  rc = resolve_split(batch, units, max_seq, &split_size);
+  rc = resolve_split(batch, heads, kv_heads, max_seq, &split_size);
   if (rc != FA_OK) return rc;
   const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
   if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
