@@ -1,7 +1,7 @@
 """Benchmark of the MI355X FlashAttention hot path (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-configs]
-                    [--only all|prefill|decode|copy]
+                    [--only all|prefill|decode|copy|gqa]
 
 Prints ONE JSON line on stdout (everything else goes to stderr):
 
@@ -313,8 +313,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config sweep")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy"], default="all",
-                    help="copy: only the 1 GiB copy that calibrates the HBM byte counters")
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy", "gqa"], default="all",
+                    help="copy: only the 1 GiB copy that calibrates the HBM byte counters; "
+                         "gqa: only the grouped-query lines")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -339,6 +340,12 @@ def main():
         log(f"1 GiB copy: {c['kernel_ms'] * 1e3:.1f} us, {c['gbs']:.1f} GB/s (read + write)")
         print(json.dumps({"metric": "device copy GB/s (counter calibration)",
                           "value": c["gbs"], "unit": "GB/s", **c}), flush=True)
+        return
+
+    if args.only == "gqa":
+        rows = bench_gqa(fa)
+        print(json.dumps({"metric": "grouped-query prefill TFLOP/s and decode KV GB/s",
+                          "value": rows[1]["gbs"], "unit": "GB/s", "gqa": rows}), flush=True)
         return
 
     result = {
