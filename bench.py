@@ -1,7 +1,7 @@
 """Benchmark of the MI355X FlashAttention hot path (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-configs]
-                    [--only all|prefill|decode|copy|gqa]
+                    [--only all|prefill|decode|copy|gqa|loop]
 
 Prints ONE JSON line on stdout (everything else goes to stderr):
 
@@ -20,6 +20,9 @@ Prints ONE JSON line on stdout (everything else goes to stderr):
 * Every timing starts with ~0.1-0.25 s of untimed launches of the same
   call, which bring the GPU to its sustained clock (an idle MI355X starts
   lower and needs ~50 ms of load to get there).
+* ``decode_loop``: tokens/s of the generation step (append_kv + decode) at
+  the reference's decode_lines shapes and the config 5 batch, eager and as a
+  replayed HIP graph.
 * ``gqa``: grouped-query prefill / decode (2 K/V heads for 14 query heads)
   at the config 3 and 5 shapes, beside the repeat-K/V-then-call path the
   reference's callers use.
@@ -238,6 +241,98 @@ def bench_gqa(fa):
     return rows
 
 
+def bench_decode_loop(fa, steps=64):
+    """Token generation: one step = append_kv (the caller's cache write) +
+    decode, starting from a context of `ctx` tokens, `steps` tokens per run.
+    bench/run_bench.py:183-210 (decode_lines) reports decode tokens/s at
+    B=1 H=12 for contexts 128-2048 on a fixed cache; here the same shapes
+    (plus the config 5 batch) run the whole step, eagerly (two host calls
+    per token) and as one captured HIP graph replayed per token (the lengths
+    live on the device, so the step's arguments never change). tokens/s =
+    batch x steps / time; `decode_ms` is decode alone on a fixed cache, the
+    reference's measurement."""
+    import torch
+
+    rows = []
+    cases = [(f"B1 H12 ctx {c}", 1, 12, c, None) for c in (128, 256, 512, 1024, 2048)]
+    cases.append(("config 5 batch B32 H14 ragged", 32, 14, 4096, "ragged"))
+    for name, batch, heads, ctx, kind in cases:
+        lmax = ctx + steps + 64
+        g = torch.Generator().manual_seed(0)
+        if kind == "ragged":
+            lens0 = torch.randint(1, ctx + 1, (batch,), generator=g).to(torch.int32)
+        else:
+            lens0 = torch.full((batch,), ctx, dtype=torch.int32)
+        kc0 = torch.randn((batch, heads, lmax, 64), generator=g).half().cuda()
+        vc0 = torch.randn((batch, heads, lmax, 64), generator=g).half().cuda()
+        qs = torch.randn((steps, batch, heads, 1, 64), generator=g).half().cuda()
+        ks = torch.randn((steps, batch, heads, 1, 64), generator=g).half().cuda()
+        vs = torch.randn((steps, batch, heads, 1, 64), generator=g).half().cuda()
+        lens0 = lens0.cuda()
+        torch.cuda.synchronize()
+
+        dec_ms = ref_timeit([lambda: fa.decode(qs[0], kc0, vc0, lens0, SCALE)])
+
+        def eager_run():
+            kc, vc, lens = kc0.clone(), vc0.clone(), lens0.clone()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for t in range(steps):
+                fa.append_kv(kc, vc, ks[t], vs[t], lens)
+                fa.decode(qs[t], kc, vc, lens, SCALE)
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / steps
+
+        eager_run()
+        eager_ms = sorted(eager_run() for _ in range(3))[1]
+
+        kc, vc, lens = kc0.clone(), vc0.clone(), lens0.clone()
+        q_in, k_in, v_in = qs[0].clone(), ks[0].clone(), vs[0].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            kw, vw, lw = kc.clone(), vc.clone(), lens.clone()
+            fa.append_kv(kw, vw, k_in, v_in, lw)
+            fa.decode(q_in, kw, vw, lw, SCALE)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fa.append_kv(kc, vc, k_in, v_in, lens)
+            fa.decode(q_in, kc, vc, lens, SCALE)
+        torch.cuda.synchronize()
+
+        def graph_run():
+            kc.copy_(kc0)
+            vc.copy_(vc0)
+            lens.copy_(lens0)
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(steps):
+                graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / steps
+
+        graph_run()
+        graph_ms = sorted(graph_run() for _ in range(3))[1]
+        rows.append({"config": name, "batch": batch, "heads": heads, "context": ctx,
+                     "steps": steps, "decode_ms": dec_ms, "decode_tok_s": batch * 1e3 / dec_ms,
+                     "step_ms_eager": eager_ms, "tok_s_eager": batch * 1e3 / eager_ms,
+                     "step_ms_graph": graph_ms, "tok_s_graph": batch * 1e3 / graph_ms})
+        log(f"  {name}: decode {dec_ms * 1e3:.1f} us; append + decode step eager "
+            f"{eager_ms * 1e3:.1f} us ({batch * 1e3 / eager_ms:,.0f} tok/s), graph "
+            f"{graph_ms * 1e3:.1f} us ({batch * 1e3 / graph_ms:,.0f} tok/s)")
+        del graph, kc, vc, kc0, vc0
+        torch.cuda.empty_cache()
+    return rows
+
+
 def cpu_baseline(budget_s=12.0):
     """The CPU oracle on a bounded sample of config 3: the 14 causal heads of
     B=1, S=4096 one at a time, cycling over them (one warm-up head first)
@@ -313,9 +408,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config sweep")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy", "gqa"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy", "gqa", "loop"],
+                    default="all",
                     help="copy: only the 1 GiB copy that calibrates the HBM byte counters; "
-                         "gqa: only the grouped-query lines")
+                         "gqa: only the grouped-query lines; loop: only the decode loop")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -340,6 +436,13 @@ def main():
         log(f"1 GiB copy: {c['kernel_ms'] * 1e3:.1f} us, {c['gbs']:.1f} GB/s (read + write)")
         print(json.dumps({"metric": "device copy GB/s (counter calibration)",
                           "value": c["gbs"], "unit": "GB/s", **c}), flush=True)
+        return
+
+    if args.only == "loop":
+        rows = bench_decode_loop(fa)
+        print(json.dumps({"metric": "decode loop tokens/s (append_kv + decode per token)",
+                          "value": rows[-1]["tok_s_graph"], "unit": "tokens/s",
+                          "decode_loop": rows}), flush=True)
         return
 
     if args.only == "gqa":
@@ -432,6 +535,8 @@ def main():
         result["configs"] = rows
         log("grouped-query attention (no reference counterpart) ...")
         result["gqa"] = bench_gqa(fa)
+        log("decode loop: append_kv + decode per token ...")
+        result["decode_loop"] = bench_decode_loop(fa)
 
     if not args.no_cpu:
         log("CPU baseline (oracle, bounded sample) ...")

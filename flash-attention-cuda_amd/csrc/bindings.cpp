@@ -229,6 +229,40 @@ at::Tensor decode_gqa_with_split(const at::Tensor &q, const at::Tensor &k_cache,
   return decode_core(q, k_cache, v_cache, seq_lens, scale, split_size, false, true);
 }
 
+// KV-cache append (no reference counterpart: its caller's cache write).
+// k_cache, v_cache [B, H_kv, Lmax, 64], k, v [B, H_kv, 1, 64], seq_lens [B]
+// int32, all on one device; updates the caches and seq_lens in place.
+void append_kv(const at::Tensor &k_cache, const at::Tensor &v_cache, const at::Tensor &k,
+               const at::Tensor &v, const at::Tensor &seq_lens) {
+  check_bhnd(k_cache, "k_cache");
+  check_bhnd(v_cache, "v_cache");
+  check_bhnd(k, "k");
+  check_bhnd(v, "v");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(),
+              "k_cache and v_cache must have identical shapes, got ", k_cache.sizes(), " and ",
+              v_cache.sizes());
+  TORCH_CHECK(k.size(2) == 1 && k.sizes() == v.sizes() && k.size(0) == k_cache.size(0) &&
+                  k.size(1) == k_cache.size(1),
+              "append_kv expects k and v of shape [B, H_kv, 1, 64] matching the caches, got k=",
+              k.sizes(), " v=", v.sizes(), " cache=", k_cache.sizes());
+  TORCH_CHECK(k_cache.size(2) > 0, "cache length must be > 0");
+  TORCH_CHECK(seq_lens.is_cuda(), "seq_lens", " must be a CUDA tensor");
+  TORCH_CHECK(seq_lens.is_contiguous(), "seq_lens", " must be contiguous row-major");
+  TORCH_CHECK(seq_lens.scalar_type() == at::kInt,
+              "seq_lens must be int32 (got ", seq_lens.scalar_type(), ")");
+  TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.size(0) == k_cache.size(0),
+              "seq_lens must be 1-D of length B=", k_cache.size(0), ", got ", seq_lens.sizes());
+  TORCH_CHECK(k_cache.device() == v_cache.device() && k_cache.device() == k.device() &&
+                  k_cache.device() == v.device() && k_cache.device() == seq_lens.device(),
+              "caches, k, v and seq_lens must live on the same device");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(k_cache.device());
+  if (k_cache.numel() == 0) return;
+  check_status(fa_kv_append(k_cache.data_ptr(), v_cache.data_ptr(), k.const_data_ptr(),
+                            v.const_data_ptr(), seq_lens.data_ptr<int32_t>(),
+                            static_cast<int>(k_cache.size(0)), static_cast<int>(k_cache.size(1)),
+                            static_cast<int>(k_cache.size(2)), stream_of(k_cache)));
+}
+
 // bindings.cpp:80-97.
 py::list occupancy_report() {
   fa_occupancy_entry rows[16];
@@ -298,6 +332,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("split_size"));
   m.def("_prefill_gqa_fp32", &prefill_gqa_fp32, py::arg("q"), py::arg("k"),
         py::arg("v"), py::arg("causal"), py::arg("scale"));
+  // KV-cache append (no reference counterpart): writes k, v at row
+  // seq_lens[b] of the caches and advances seq_lens, on the device.
+  m.def("append_kv", &append_kv,
+        "Write one token's K/V at row seq_lens[b] of the caches and advance seq_lens",
+        py::arg("k_cache"), py::arg("v_cache"), py::arg("k"), py::arg("v"),
+        py::arg("seq_lens"));
   m.def("_decode_gqa_fp32", &decode_gqa_fp32, py::arg("q"), py::arg("k_cache"),
         py::arg("v_cache"), py::arg("seq_lens"), py::arg("scale"),
         py::arg("split_size") = 0);

@@ -52,6 +52,12 @@ int decode_units_per_row(int heads, int kv_heads);
 // multiples of 32 rows, at least 64.
 int decode_group_chunk(int batch, int units_per_row, int max_seq);
 
+// Writes k_new / v_new ([B, H_kv, 1, 64]) at row seq_lens[b] of the caches
+// and advances seq_lens[b] (kv_cache.hip).
+int launch_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
+                     int32_t *seq_lens, int batch, int kv_heads, int max_seq,
+                     hipStream_t stream);
+
 // Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);
 int decode_occupancy(fa_occupancy_entry *out, int cap, int *n);

@@ -306,6 +306,28 @@ int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
                      max_seq, scale, split_size, workspace, workspace_bytes, stream);
 }
 
+int fa_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
+                 int32_t *seq_lens, int batch, int kv_heads, int max_seq, void *stream) {
+  clear_error();
+  if (k_cache == nullptr || v_cache == nullptr || k_new == nullptr || v_new == nullptr ||
+      seq_lens == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "k_cache, v_cache, k_new, v_new and seq_lens must be non-NULL");
+  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(k_new) || !aligned16(v_new))
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "k_cache, v_cache, k_new and v_new must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "seq_lens must be 4-byte aligned");
+  if (batch <= 0 || kv_heads <= 0)
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "batch and kv_heads must be > 0, got B=%d H_kv=%d", batch, kv_heads);
+  if (max_seq <= 0 || max_seq > kMaxCacheRows)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be in [1, %d], got %d",
+                     kMaxCacheRows, max_seq);
+  return launch_kv_append(k_cache, v_cache, k_new, v_new, seq_lens, batch, kv_heads, max_seq,
+                          static_cast<hipStream_t>(stream));
+}
+
 int fa_occupancy_report(fa_occupancy_entry *out, int capacity, int *count) {
   clear_error();
   if (count == nullptr || (capacity > 0 && out == nullptr))

@@ -12,6 +12,11 @@ dividing H; query head h reads K/V head h // (H // H_kv), as
 ``k.repeat_interleave(H // H_kv, dim=1)`` would pair them), without
 materialising the repeated K/V.
 
+Also added: ``append_kv(k_cache, v_cache, k, v, seq_lens)``, the caller's
+cache write before a decode step (row ``seq_lens[b]``, then ``seq_lens[b] +=
+1``, on the device), so a whole append + decode step can be captured in a
+HIP graph and replayed per token.
+
 The v1 ``legacy_naive/tiled/fused`` teaching kernels of the reference are
 not part of this build; touching them raises ``NotImplementedError``.
 
@@ -31,6 +36,7 @@ try:
         _decode_with_split,
         _prefill_fp32,
         _prefill_gqa_fp32,
+        append_kv,
         choose_decode_split,
         decode,
         decode_gqa,
@@ -60,6 +66,7 @@ __all__ = [
     "decode",
     "prefill_gqa",
     "decode_gqa",
+    "append_kv",
     "head_dim",
     "occupancy_report",
     "choose_decode_split",

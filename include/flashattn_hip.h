@@ -29,6 +29,9 @@
  *                               attention is future work in the reference
  *                               (README.md:398); its callers repeat K/V per
  *                               query head and call prefill / decode.
+ *   fa_kv_append             <- no counterpart: the cache write its caller
+ *                               (the FlashStack engine, README.md:9-13) does
+ *                               before each decode step.
  *
  * Tensor layout (same as the reference): q, k, v, o are [B, H, S, 64]
  * contiguous fp16 (IEEE binary16); a decode cache is [B, H, Lmax, 64]; the
@@ -139,6 +142,18 @@ int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
                   int heads, int kv_heads, int max_seq, float scale,
                   int split_size, void *workspace, size_t workspace_bytes,
                   void *stream);
+
+/* KV-cache append, the caller step before a decode: for every batch row b
+ * with 0 <= seq_lens[b] < max_seq, write k_new[b, h] / v_new[b, h]
+ * ([B, H_kv, 1, 64]) into row seq_lens[b] of k_cache / v_cache
+ * ([B, H_kv, max_seq, 64]) for every K/V head h, then set
+ * seq_lens[b] += 1, all on the device (seq_lens is never read on the host).
+ * Rows with seq_lens[b] < 0 or >= max_seq are left alone, lengths included.
+ * The lengths live only in device memory, so an append + decode step has
+ * the same arguments for every token and can be captured in a HIP graph. */
+int fa_kv_append(void *k_cache, void *v_cache, const void *k_new,
+                 const void *v_new, int32_t *seq_lens, int batch, int kv_heads,
+                 int max_seq, void *stream);
 
 /* Fill up to `capacity` entries (one per kernel) for the current device;
  * *count receives the number of kernels. Returns an fa_status. */

@@ -14,6 +14,7 @@ from .attention import (  # noqa: F401
     decode_gqa,
     fp16_half_ulp,
     fp16_rounding_floor,
+    kv_append,
     make_decode_inputs,
     make_prefill_inputs,
     prefill,

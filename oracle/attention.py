@@ -24,6 +24,10 @@ What it restates (paths relative to shrvan30/flash-attention-cuda):
   reads K/V head h // (H // H_kv), the pairing of
   ``repeat_interleave(H // H_kv, dim=1)``; restated as ``prefill`` /
   ``decode`` on the repeated K/V.
+* ``kv_append``: the cache write the reference's caller performs before each
+  decode step (README.md:9-13: the FlashStack engine writes token t at row
+  seq_lens[b]); restated as: for 0 <= seq_lens[b] < Lmax, row seq_lens[b] of
+  every K/V head of sequence b takes the new token, then seq_lens[b] += 1.
 * ``choose_decode_split``: csrc/decode.cu:183-192 (integer closed form).
 * ``attention_flops``: bench/run_bench.py:102-107 (4 B H N^2 d, halved when
   causal). ``decode_bytes``: K and V rows actually read plus q, o, seq_lens.
@@ -137,6 +141,23 @@ def decode_gqa(q, k_cache, v_cache, seq_lens, scale: float) -> np.ndarray:
     """``decode`` with caches of shape [B, H_kv, Lmax, 64] (H_kv divides H)."""
     heads = np.asarray(q).shape[1]
     return decode(q, repeat_kv(k_cache, heads), repeat_kv(v_cache, heads), seq_lens, scale)
+
+
+def kv_append(k_cache, v_cache, k_new, v_new, seq_lens):
+    """Returns (k_cache, v_cache, seq_lens) after appending one token per
+    sequence: k_new, v_new are [B, H_kv, 1, 64]; sequences whose length is
+    negative or already Lmax are left unchanged. The inputs are not modified."""
+    k_cache = np.array(k_cache, copy=True)
+    v_cache = np.array(v_cache, copy=True)
+    lens = np.array(seq_lens, dtype=np.int32, copy=True)
+    lmax = k_cache.shape[2]
+    for b in range(lens.shape[0]):
+        n = int(lens[b])
+        if 0 <= n < lmax:
+            k_cache[b, :, n] = np.asarray(k_new)[b, :, 0]
+            v_cache[b, :, n] = np.asarray(v_new)[b, :, 0]
+            lens[b] = n + 1
+    return k_cache, v_cache, lens
 
 
 def choose_decode_split(max_seq: int, batch: int, heads: int, min_blocks: int) -> int:

@@ -55,6 +55,7 @@ def test_header_declares_the_expected_entry_points():
             "fa_decode_min_blocks",
             "fa_decode_workspace_bytes",
             "fa_head_dim",
+            "fa_kv_append",
             "fa_last_error",
             "fa_occupancy_report",
             "fa_prefill",
@@ -153,13 +154,28 @@ def test_grouped_decode_workspace_holds_one_partial_per_query_head(lib):
     assert lib.fa_decode_gqa_workspace_bytes(1, 12, 4, 4096, 128) == 12 * 32 * 66 * 4
 
 
+def test_kv_append_rejects_bad_arguments_before_any_launch(lib):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    rc = lib.fa_kv_append(p, p, p, None, p, 1, 1, 8, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"non-NULL" in lib.fa_last_error()
+    rc = lib.fa_kv_append(p, p, ctypes.c_void_p(p.value + 8), p, p, 1, 1, 8, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"16-byte aligned" in lib.fa_last_error()
+    rc = lib.fa_kv_append(p, p, p, p, ctypes.c_void_p(p.value + 2), 1, 1, 8, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"4-byte aligned" in lib.fa_last_error()
+    rc = lib.fa_kv_append(p, p, p, p, p, 1, 0, 8, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"must be > 0" in lib.fa_last_error()
+    rc = lib.fa_kv_append(p, p, p, p, p, 1, 1, 0, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"cache length must be in [1, " in lib.fa_last_error()
+
+
 def test_python_package_exposes_reference_surface():
     """flashattn_cuda/__init__.py:20-29 of the reference (legacy_* stubbed)."""
     import flashattn_cuda as fa
 
     for name in ("prefill", "decode", "head_dim", "occupancy_report", "choose_decode_split",
                  "_decode_with_split", "legacy_naive", "legacy_tiled", "legacy_fused",
-                 "prefill_gqa", "decode_gqa"):
+                 "prefill_gqa", "decode_gqa", "append_kv"):
         assert hasattr(fa, name), name
     assert fa.head_dim == 64 and fa.__version__ == "2.0.0"
     assert fa.choose_decode_split(512, 1, 12, 512) == 128

@@ -383,3 +383,78 @@ def test_decode_gqa_equals_causal_prefill_gqa_row():
     got = oracle.decode_gqa(q[:, :, 11:12], k, v, lens, 0.125)
     assert not got[0].any()
     assert np.abs(got[1] - full[1, :, 11:12]).max() < 2e-6
+
+
+# ---------------------------------------------------------------------------
+# KV-cache append: the caller step before decode.
+# ---------------------------------------------------------------------------
+
+
+def test_kv_append_writes_row_len_and_advances():
+    k = np.zeros((4, 2, 5, 64), np.float16)
+    v = np.zeros((4, 2, 5, 64), np.float16)
+    kn = _rand((4, 2, 1, 64), 60).numpy()
+    vn = _rand((4, 2, 1, 64), 61).numpy()
+    lens = np.array([0, 3, 5, -1], np.int32)  # empty, middle, full, negative
+    k2, v2, l2 = oracle.kv_append(k, v, kn, vn, lens)
+    assert l2.tolist() == [1, 4, 5, -1]
+    assert np.array_equal(k2[0, :, 0], kn[0, :, 0]) and np.array_equal(v2[1, :, 3], vn[1, :, 0])
+    # Nothing else moved: rows other than the written ones, the full and the
+    # negative sequences, and the inputs themselves.
+    mask = np.zeros(k.shape, bool)
+    mask[0, :, 0] = mask[1, :, 3] = True
+    assert not k2[~mask].any() and not v2[~mask].any()
+    assert not k.any() and lens.tolist() == [0, 3, 5, -1]
+
+
+def _incremental_matches_prefill(append_fn, heads, kv_heads):
+    S = 9
+    q = _rand((2, heads, S, 64), 62).numpy()
+    k = _rand((2, kv_heads, S, 64), 63).numpy()
+    v = _rand((2, kv_heads, S, 64), 64).numpy()
+    full = oracle.prefill_gqa(q, k, v, True, 0.125)
+    kc = np.zeros((2, kv_heads, 12, 64), np.float16)
+    vc = np.zeros_like(kc)
+    lens = np.zeros(2, np.int32)
+    for t in range(S):
+        kc, vc, lens = append_fn(kc, vc, k[:, :, t : t + 1], v[:, :, t : t + 1], lens)
+        out = oracle.decode_gqa(q[:, :, t : t + 1], kc, vc, lens, 0.125)
+        assert np.abs(out - full[:, :, t : t + 1]).max() < 2e-6, t
+
+
+@pytest.mark.parametrize("kind", ["row_after_len", "advance_before_write", "k_into_v"])
+def test_planted_kv_append_mistakes_are_caught(kind):
+    def bad(kc, vc, kn, vn, lens):
+        kc, vc, lens = kc.copy(), vc.copy(), lens.copy()
+        for b in range(lens.shape[0]):
+            n = int(lens[b])
+            row = n + 1 if kind in ("row_after_len", "advance_before_write") else n
+            if kind == "advance_before_write":
+                row = min(row, kc.shape[2] - 1)
+            kc[b, :, row] = kn[b, :, 0]
+            vc[b, :, row] = (kn if kind == "k_into_v" else vn)[b, :, 0]
+            lens[b] = n + 1
+        return kc, vc, lens
+
+    with pytest.raises(AssertionError):
+        _incremental_matches_prefill(bad, 6, 2)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(3, 3), (6, 2)])
+def test_incremental_decode_through_kv_append_equals_causal_prefill(heads, kv_heads):
+    """Generating token by token (append, then decode over the cache) gives
+    the rows of causal prefill over the whole sequence (tests:94-110 form)."""
+    _incremental_matches_prefill(oracle.kv_append, heads, kv_heads)
+    S = 9
+    q = _rand((2, heads, S, 64), 62).numpy()
+    k = _rand((2, kv_heads, S, 64), 63).numpy()
+    v = _rand((2, kv_heads, S, 64), 64).numpy()
+    full = oracle.prefill_gqa(q, k, v, True, 0.125)
+    kc = np.zeros((2, kv_heads, 12, 64), np.float16)
+    vc = np.zeros_like(kc)
+    lens = np.zeros(2, np.int32)
+    for t in range(S):
+        kc, vc, lens = oracle.kv_append(kc, vc, k[:, :, t : t + 1], v[:, :, t : t + 1], lens)
+        out = oracle.decode_gqa(q[:, :, t : t + 1], kc, vc, lens, 0.125)
+        assert np.abs(out - full[:, :, t : t + 1]).max() < 2e-6, t
+    assert lens.tolist() == [S, S]

@@ -225,7 +225,22 @@ def _ragged_lens(batch, max_seq, seed):
     return lens
 
 
-# B * H >= compute units selects the whole-sequence kernel (one block per
+def test_decode_split_path_edges():
+    """The split-K pass (B * H below the CU count, Lmax > 512) on edge
+    lengths: empty, negative, past the cache, exactly the cache, 1, 63-65."""
+    lens = _ragged_lens(9, 1000, seed=24)
+    q, k, v, lens = oracle.make_decode_inputs(9, 2, 1000, seed=25, lens=lens)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    out16 = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+    out32 = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    _check(out16, out32, ref, "split path edges B9 H2 L1000")
+    o = out32.cpu().numpy()
+    assert not o[0].any() and not o[1].any()
+
+
+# B * H >= compute units (or Lmax <= 512) selects the whole-sequence kernel (one block per
 # (b, h)); these shapes cover its resident grid (every block on the chip at
 # once), its oversubscribed grid, and a batch too large for the in-block
 # length ranking.
