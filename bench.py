@@ -391,11 +391,13 @@ def copy_calibration(steps):
 
 
 def load_traffic(name):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    """HBM bytes per launch of a workload's main kernel, from the committed
+    rocprofv3 report (profiles/<workload>__<kernel>.md, written by
+    flash-attention-cuda_amd/profile/profile_rocprof.sh), if present."""
     path = os.path.join(REPO, "profiles", name)
     if not os.path.exists(path):
         return None
-    for line in open(path):
+    for line in open(path, encoding="utf-8"):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
@@ -486,7 +488,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
             "kernel_ms": r["kernel_ms"],
-            "traffic": load_traffic("prefill_c3_traffic.txt"),
+            "traffic": load_traffic("prefill_c3__prefill_kernel.md"),
         }
         log(f"  {value:.1f} TFLOP/s per step, kernel {achieved:.1f} TFLOP/s "
             f"({100 * achieved / MFMA_FP16_PEAK_TFLOPS:.1f}% of MFMA peak)")
@@ -508,7 +510,7 @@ def main():
             "roofline": {"bound": "hbm", "kernel": "decode_bh_kernel",
                          "achieved": gbs_kern, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs_kern / HBM_PEAK_GBS, "kernel_ms": d["kernel_ms"],
-                         "traffic": load_traffic("decode_c5_traffic.txt")},
+                         "traffic": load_traffic("decode_c5__decode_bh_kernel.md")},
         }
         if args.only == "decode":
             result["value"], result["unit"] = gbs_step, "GB/s"
