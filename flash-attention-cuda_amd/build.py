@@ -30,7 +30,7 @@ INCLUDE = os.path.join(REPO_ROOT, "include")
 OUT_DIR = os.path.join(PKG_ROOT, "flashattn_cuda")
 BUILD_DIR = os.path.join(PKG_ROOT, "_build")
 
-HIP_SOURCES = ["runtime.hip", "prefill.hip", "decode.hip", "kv_cache.hip"]
+HIP_SOURCES = ["runtime.hip", "prefill.hip", "decode.hip", "kv_cache.hip", "legacy.hip"]
 LIB_NAME = "libflashattn_hip.so"
 ARCH = os.environ.get("FA_OFFLOAD_ARCH", "gfx950")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")

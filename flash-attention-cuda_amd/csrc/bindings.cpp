@@ -10,7 +10,9 @@
 // empty_like(q), asynchronous launch on the current stream, no host sync.
 // Added: a device guard for inputs that live on a non-current device, the
 // fp32-output parity hooks `_prefill_fp32` / `_decode_fp32`, and grouped-query
-// variants `prefill_gqa` / `decode_gqa` (K/V with fewer heads than Q).
+// variants `prefill_gqa` / `decode_gqa` (K/V with fewer heads than Q). The v1
+// legacy_naive / legacy_tiled / legacy_fused kernels (csrc/legacy/) keep
+// their own checks and messages (legacy_ops.cu:19-35).
 //
 // Torch-ROCm calls the HIP device "cuda", so `is_cuda()` is the right check
 // and the reference's messages stay verbatim; the device guard and stream
@@ -282,13 +284,55 @@ py::list occupancy_report() {
   return out;
 }
 
+// csrc/legacy/legacy_ops.cu:19-51: the v1 single-head fp32 kernels, with the
+// reference's check order and messages; the output is empty_like(q).
+void check_legacy_inputs(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(),
+              "legacy kernels expect CUDA tensors");
+  TORCH_CHECK(q.scalar_type() == at::kFloat && k.scalar_type() == at::kFloat &&
+                  v.scalar_type() == at::kFloat,
+              "legacy kernels are fp32 only");
+  TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
+              "legacy kernels expect contiguous tensors");
+  TORCH_CHECK(q.dim() == 2 && k.dim() == 2 && v.dim() == 2,
+              "legacy kernels are single-head: expected (N, ", kHeadDim, ") tensors");
+  TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
+              "legacy kernels expect identical q/k/v shapes");
+  TORCH_CHECK(q.size(1) == kHeadDim, "legacy kernels expect head_dim == ", kHeadDim);
+  TORCH_CHECK(q.device() == k.device() && q.device() == v.device(),
+              "legacy kernels expect q, k and v on the same device");
+}
+
+at::Tensor legacy_impl(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
+                       int variant) {
+  check_legacy_inputs(q, k, v);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  at::Tensor o = at::empty_like(q);
+  if (q.size(0) == 0) return o;  // empty tensors carry no data pointer
+  TORCH_CHECK(q.size(0) < (int64_t{1} << 31) / kHeadDim, "legacy kernels: too many rows");
+  check_status(fa_legacy_attention(q.const_data_ptr<float>(), k.const_data_ptr<float>(),
+                                   v.const_data_ptr<float>(), o.data_ptr<float>(),
+                                   static_cast<int>(q.size(0)), variant, stream_of(q)));
+  return o;
+}
+
+at::Tensor legacy_naive(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v) {
+  return legacy_impl(q, k, v, FA_LEGACY_NAIVE);
+}
+at::Tensor legacy_tiled(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v) {
+  return legacy_impl(q, k, v, FA_LEGACY_TILED);
+}
+at::Tensor legacy_fused(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v) {
+  return legacy_impl(q, k, v, FA_LEGACY_FUSED);
+}
+
 int choose_decode_split(int max_seq, int batch, int heads, int min_blocks) {
   return fa_choose_decode_split(max_seq, batch, heads, min_blocks);
 }
 
 }  // namespace
 
-// bindings.cpp:110-134 (minus the out-of-scope v1 legacy_* kernels).
+// bindings.cpp:110-134.
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Batched multi-head causal FlashAttention kernels for head_dim=64 "
             "(MI355X / gfx950)";
@@ -341,4 +385,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_decode_gqa_fp32", &decode_gqa_fp32, py::arg("q"), py::arg("k_cache"),
         py::arg("v_cache"), py::arg("seq_lens"), py::arg("scale"),
         py::arg("split_size") = 0);
+
+  // bindings.cpp:131-133: the v1 kernels, (N, 64) fp32, one head, no mask.
+  m.def("legacy_naive", &legacy_naive, "v1 naive kernel (N, 64) fp32");
+  m.def("legacy_tiled", &legacy_tiled, "v1 tiled kernel (N, 64) fp32");
+  m.def("legacy_fused", &legacy_fused, "v1 fused kernel (N, 64) fp32");
 }

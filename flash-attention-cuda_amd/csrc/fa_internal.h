@@ -58,6 +58,11 @@ int launch_kv_append(void *k_cache, void *v_cache, const void *k_new, const void
                      int32_t *seq_lens, int batch, int kv_heads, int max_seq,
                      hipStream_t stream);
 
+// o = softmax(q k^T / 8) v for one (n, 64) fp32 head, no mask; variant is an
+// fa_legacy_variant (legacy.hip).
+int launch_legacy_attention(const float *q, const float *k, const float *v, float *o, int n,
+                            int variant, hipStream_t stream);
+
 // Occupancy rows for each kernel (appended to `out`, at most `cap` rows).
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n);
 int decode_occupancy(fa_occupancy_entry *out, int cap, int *n);

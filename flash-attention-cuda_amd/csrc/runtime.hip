@@ -328,6 +328,22 @@ int fa_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_
                           static_cast<hipStream_t>(stream));
 }
 
+int fa_legacy_attention(const float *q, const float *k, const float *v, float *o, int n,
+                        int variant, void *stream) {
+  clear_error();
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "q, k, v and o must be 16-byte aligned device pointers");
+  if (variant != FA_LEGACY_NAIVE && variant != FA_LEGACY_TILED && variant != FA_LEGACY_FUSED)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "unknown legacy variant %d", variant);
+  if (n < 0 || static_cast<int64_t>(n) * kHeadDim > 0x7fffffffll)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "row count must be in [0, 2^31 / 64), got %d", n);
+  if (n == 0) return FA_OK;  // nothing to compute, nothing launched
+  return launch_legacy_attention(q, k, v, o, n, variant, static_cast<hipStream_t>(stream));
+}
+
 int fa_occupancy_report(fa_occupancy_entry *out, int capacity, int *count) {
   clear_error();
   if (count == nullptr || (capacity > 0 && out == nullptr))

@@ -17,8 +17,8 @@ cache write before a decode step (row ``seq_lens[b]``, then ``seq_lens[b] +=
 1``, on the device), so a whole append + decode step can be captured in a
 HIP graph and replayed per token.
 
-The v1 ``legacy_naive/tiled/fused`` teaching kernels of the reference are
-not part of this build; touching them raises ``NotImplementedError``.
+The v1 ``legacy_naive/tiled/fused`` kernels of the reference (one (N, 64)
+fp32 head, no mask, scale 1/8) are there too, with the reference's checks.
 
 There is no fallback: if the compiled extension ``_C`` (and the HIP library
 ``libflashattn_hip.so`` it links) is missing, importing this package fails.
@@ -41,6 +41,9 @@ try:
         decode,
         decode_gqa,
         head_dim,
+        legacy_fused,
+        legacy_naive,
+        legacy_tiled,
         occupancy_report,
         prefill,
         prefill_gqa,
@@ -52,14 +55,6 @@ except ImportError as exc:  # pragma: no cover - exercised only when unbuilt
         f"first. Underlying error: {exc}"
     ) from exc
 
-
-def _legacy_unavailable(*_args, **_kwargs):
-    raise NotImplementedError(
-        "the v1 legacy_* fp32 teaching kernels are not part of the MI355X build"
-    )
-
-
-legacy_naive = legacy_tiled = legacy_fused = _legacy_unavailable
 
 __all__ = [
     "prefill",

@@ -32,6 +32,11 @@
  *   fa_kv_append             <- no counterpart: the cache write its caller
  *                               (the FlashStack engine, README.md:9-13) does
  *                               before each decode step.
+ *   fa_legacy_attention      <- launch_naive_attention / launch_tiled_attention /
+ *                               launch_fused_attention,
+ *                               src/legacy/{naive,tiled,fused}_attention.cu
+ *                               (called by legacy_naive / legacy_tiled /
+ *                               legacy_fused, csrc/legacy/legacy_ops.cu:38-51)
  *
  * Tensor layout (same as the reference): q, k, v, o are [B, H, S, 64]
  * contiguous fp16 (IEEE binary16); a decode cache is [B, H, Lmax, 64]; the
@@ -154,6 +159,22 @@ int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
 int fa_kv_append(void *k_cache, void *v_cache, const void *k_new,
                  const void *v_new, int32_t *seq_lens, int batch, int kv_heads,
                  int max_seq, void *stream);
+
+/* The reference's v1 single-head kernels: o = softmax(q k^T / sqrt(64)) v
+ * for q, k, v, o of shape (n, 64) fp32, row-major, no mask. The three
+ * variants compute the same function (results agree to fp32 rounding):
+ * FA_LEGACY_NAIVE takes the exact row max in a first pass, FA_LEGACY_TILED
+ * and FA_LEGACY_FUSED an online softmax (O renormalised per tile, resp.
+ * divided once at the end). n == 0 launches nothing. Asynchronous on
+ * `stream` like every other entry point (the v1 launchers synchronised). */
+typedef enum fa_legacy_variant {
+  FA_LEGACY_NAIVE = 0,
+  FA_LEGACY_TILED = 1,
+  FA_LEGACY_FUSED = 2
+} fa_legacy_variant;
+
+int fa_legacy_attention(const float *q, const float *k, const float *v,
+                        float *o, int n, int variant, void *stream);
 
 /* Fill up to `capacity` entries (one per kernel) for the current device;
  * *count receives the number of kernels. Returns an fa_status. */

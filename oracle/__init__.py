@@ -15,6 +15,7 @@ from .attention import (  # noqa: F401
     fp16_half_ulp,
     fp16_rounding_floor,
     kv_append,
+    legacy_attention,
     make_decode_inputs,
     make_prefill_inputs,
     prefill,

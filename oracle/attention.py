@@ -28,6 +28,11 @@ What it restates (paths relative to shrvan30/flash-attention-cuda):
   decode step (README.md:9-13: the FlashStack engine writes token t at row
   seq_lens[b]); restated as: for 0 <= seq_lens[b] < Lmax, row seq_lens[b] of
   every K/V head of sequence b takes the new token, then seq_lens[b] += 1.
+* ``legacy_attention``: the function the reference's v1 kernels compute
+  (src/legacy/naive_attention.cu:45-110, tiled_attention.cu:28-205,
+  fused_attention.cu:54-200, launched with scale 1/sqrt(d) by
+  :139 / :240 / :213): one (N, 64) fp32 head, no mask -- ``attention_cpu``
+  with its default scale.
 * ``choose_decode_split``: csrc/decode.cu:183-192 (integer closed form).
 * ``attention_flops``: bench/run_bench.py:102-107 (4 B H N^2 d, halved when
   causal). ``decode_bytes``: K and V rows actually read plus q, o, seq_lens.
@@ -119,6 +124,19 @@ def decode(q, k_cache, v_cache, seq_lens, scale: float) -> np.ndarray:
         for h in range(H):
             out[b, h] = attention_cpu(q[b, h], k_cache[b, h, :n], v_cache[b, h, :n], scale)
     return out
+
+
+def legacy_attention(q, k, v) -> np.ndarray:
+    """(N, 64) fp32 -> (N, 64) fp32: softmax(q k^T / sqrt(64)) v, no mask.
+
+    The v1 kernels (src/legacy/*_attention.cu) take no scale argument; their
+    launchers pass 1 / sqrt(d) (naive_attention.cu:139, tiled_attention.cu:240,
+    fused_attention.cu:213).
+    """
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    return attention_cpu(q, k, v, scale=None, causal=False)
 
 
 def repeat_kv(x, heads: int) -> np.ndarray:

@@ -57,6 +57,7 @@ def test_header_declares_the_expected_entry_points():
             "fa_head_dim",
             "fa_kv_append",
             "fa_last_error",
+            "fa_legacy_attention",
             "fa_occupancy_report",
             "fa_prefill",
             "fa_prefill_gqa",
@@ -169,8 +170,22 @@ def test_kv_append_rejects_bad_arguments_before_any_launch(lib):
     assert rc == FA_ERR_INVALID_ARGUMENT and b"cache length must be in [1, " in lib.fa_last_error()
 
 
+def test_legacy_attention_argument_checks(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.fa_legacy_attention(None, p, p, p, 8, 0, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"non-NULL" in lib.fa_last_error()
+    rc = lib.fa_legacy_attention(ctypes.c_void_p(4100), p, p, p, 8, 0, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"16-byte aligned" in lib.fa_last_error()
+    rc = lib.fa_legacy_attention(p, p, p, p, 8, 3, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"unknown legacy variant" in lib.fa_last_error()
+    rc = lib.fa_legacy_attention(p, p, p, p, -1, 0, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"row count" in lib.fa_last_error()
+    # n == 0 computes nothing and launches nothing (no device needed).
+    assert lib.fa_legacy_attention(p, p, p, p, 0, 2, None) == FA_OK
+
+
 def test_python_package_exposes_reference_surface():
-    """flashattn_cuda/__init__.py:20-29 of the reference (legacy_* stubbed)."""
+    """flashattn_cuda/__init__.py:20-29 of the reference."""
     import flashattn_cuda as fa
 
     for name in ("prefill", "decode", "head_dim", "occupancy_report", "choose_decode_split",
@@ -180,8 +195,12 @@ def test_python_package_exposes_reference_surface():
     assert fa.head_dim == 64 and fa.__version__ == "2.0.0"
     assert fa.choose_decode_split(512, 1, 12, 512) == 128
     assert fa.choose_decode_split(max_seq=4096, batch=32, heads=14, min_blocks=512) == 1024
-    with pytest.raises(NotImplementedError):
-        fa.legacy_fused(None, None, None)
+    import torch
+
+    x = torch.zeros(4, 64)
+    for fn in (fa.legacy_naive, fa.legacy_tiled, fa.legacy_fused):
+        with pytest.raises(RuntimeError, match="legacy kernels expect CUDA tensors"):
+            fn(x, x, x)
 
 
 def test_python_rejects_cpu_tensors_without_a_device():

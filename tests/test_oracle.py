@@ -114,6 +114,52 @@ def test_default_scale_is_inverse_sqrt_d():
     np.testing.assert_allclose(oracle.attention_cpu(Q, K, V), oracle.attention_cpu(Q, K, V, 0.125), rtol=0, atol=0)
 
 
+def _legacy_fp64_loop(Q, K, V):
+    """softmax(Q K^T / 8) V by explicit fp64 loops (the v1 kernels' function)."""
+    out = np.empty(Q.shape, dtype=np.float64)
+    for i in range(Q.shape[0]):
+        s = [sum(float(Q[i, d]) * float(K[j, d]) for d in range(D)) / 8.0 for j in range(K.shape[0])]
+        m = max(s)
+        w = [math.exp(x - m) for x in s]
+        for d in range(D):
+            out[i, d] = sum(w[j] * float(V[j, d]) for j in range(K.shape[0])) / sum(w)
+    return out
+
+
+def test_legacy_attention_matches_fp64_loop():
+    """legacy_attention: (N, 64) fp32, scale 1/sqrt(64), no mask
+    (src/legacy/*_attention.cu; launchers at naive :139, tiled :240, fused :213)."""
+    rng = np.random.default_rng(11)
+    Q, K, V = (rng.standard_normal((7, D)).astype(np.float32) for _ in range(3))
+    got = oracle.legacy_attention(Q, K, V)
+    assert got.dtype == np.float32 and got.shape == (7, D)
+    assert np.abs(got - _legacy_fp64_loop(Q, K, V)).max() < 2e-6
+    # One row: the output is that value row exactly; equal keys: the mean of V.
+    np.testing.assert_array_equal(oracle.legacy_attention(Q[:1], K[:1], V[:1]), V[:1])
+    same = np.repeat(K[:1], 5, axis=0)
+    np.testing.assert_allclose(oracle.legacy_attention(Q[:2], same, V[:5]),
+                               np.repeat(V[:5].mean(0, keepdims=True), 2, 0), atol=1e-6)
+
+
+@pytest.mark.parametrize("kind", ["scale_1_over_64", "causal", "no_max_shift_overflow"])
+def test_planted_legacy_mistakes_are_caught(kind):
+    rng = np.random.default_rng(12)
+    Q, K, V = (rng.standard_normal((6, D)).astype(np.float32) for _ in range(3))
+    if kind == "no_max_shift_overflow":
+        Q = Q * 40.0  # scores ~ 300: exp without the max shift overflows
+    want = _legacy_fp64_loop(Q, K, V)
+    if kind == "scale_1_over_64":
+        bad = oracle.attention_cpu(Q, K, V, 1.0 / 64)
+    elif kind == "causal":
+        bad = oracle.attention_cpu(Q, K, V, None, True)
+    else:
+        with np.errstate(over="ignore", invalid="ignore"):
+            e = np.exp((Q @ K.T) / 8.0)
+            bad = (e / e.sum(1, keepdims=True)) @ V
+    assert not (np.abs(bad - want).max() < 1e-4)
+    assert np.abs(oracle.legacy_attention(Q, K, V) - want).max() < 1e-4
+
+
 def test_stable_softmax_rows_and_shift_invariance():
     x = np.array([[1.0, 2.0, 3.0], [1000.0, 1001.0, -np.inf]], dtype=np.float32)
     p = oracle.stable_softmax(x)
