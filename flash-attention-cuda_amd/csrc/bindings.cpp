@@ -8,7 +8,9 @@
 // contiguous", "head_dim", "identical shapes", "exactly one query row",
 // "seq_lens must be int32", "seq_lens must be 1-D"), output allocation with
 // empty_like(q), asynchronous launch on the current stream, no host sync.
-// Added: a device guard for inputs that live on a non-current device, the
+// Added: head_dim 128 for prefill / decode / append_kv (the head size is
+// read from the tensors; `head_dim` stays 64, `head_dims` lists both), a
+// device guard for inputs that live on a non-current device, the
 // fp32-output parity hooks `_prefill_fp32` / `_decode_fp32`, and grouped-query
 // variants `prefill_gqa` / `decode_gqa` (K/V with fewer heads than Q). The v1
 // legacy_naive / legacy_tiled / legacy_fused kernels (csrc/legacy/) keep
@@ -32,7 +34,9 @@ namespace {
 
 constexpr int kHeadDim = FA_HEAD_DIM;
 
-// flash_common.h:43-62 of the reference.
+// flash_common.h:43-62 of the reference. The head size may also be 128 here
+// (the reference's named next step, README.md:397); any other size fails
+// with a "head_dim" message as in the reference.
 void check_bhnd(const at::Tensor &t, const char *name) {
   TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
   TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be fp16 (got ",
@@ -40,8 +44,8 @@ void check_bhnd(const at::Tensor &t, const char *name) {
   TORCH_CHECK(t.is_contiguous(), name, " must be contiguous row-major");
   TORCH_CHECK(t.dim() == 4, name, " must be 4-D (B, H, N, ", kHeadDim,
               "), got ", t.dim(), "-D");
-  TORCH_CHECK(t.size(3) == kHeadDim, name, " must have head_dim == ", kHeadDim,
-              ", got ", t.size(3));
+  TORCH_CHECK(t.size(3) == kHeadDim || t.size(3) == 128, name,
+              " must have head_dim == ", kHeadDim, " (or 128), got ", t.size(3));
 }
 
 void check_status(int rc) {
@@ -72,6 +76,9 @@ at::Tensor prefill_impl(const at::Tensor &q, const at::Tensor &k,
     TORCH_CHECK(k.size(1) > 0 && q.size(1) % k.size(1) == 0,
                 "prefill_gqa expects the K/V head count to divide the query head count, "
                 "got H=", q.size(1), " H_kv=", k.size(1));
+    TORCH_CHECK(q.size(3) == k.size(3),
+                "prefill_gqa expects q and k/v to have the same head_dim, got ", q.size(3),
+                " and ", k.size(3));
   } else {
     TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
                 "prefill expects q, k and v to have identical shapes, got q=",
@@ -92,16 +99,16 @@ at::Tensor prefill_impl(const at::Tensor &q, const at::Tensor &k,
   at::Tensor ws;
   if (ws_bytes > 0)
     ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-  check_status(fa_prefill_gqa(q.const_data_ptr(), k.const_data_ptr(),
-                              v.const_data_ptr(), o.data_ptr(),
-                              out_f32 ? FA_OUT_F32 : FA_OUT_F16,
-                              static_cast<int>(q.size(0)),
-                              static_cast<int>(q.size(1)),
-                              static_cast<int>(k.size(1)),
-                              static_cast<int>(q.size(2)), causal ? 1 : 0,
-                              static_cast<float>(scale),
-                              ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
-                              stream_of(q)));
+  check_status(fa_prefill_hd(q.const_data_ptr(), k.const_data_ptr(),
+                             v.const_data_ptr(), o.data_ptr(),
+                             out_f32 ? FA_OUT_F32 : FA_OUT_F16,
+                             static_cast<int>(q.size(0)),
+                             static_cast<int>(q.size(1)),
+                             static_cast<int>(k.size(1)),
+                             static_cast<int>(q.size(2)), static_cast<int>(q.size(3)),
+                             causal ? 1 : 0, static_cast<float>(scale),
+                             ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                             stream_of(q)));
   return o;
 }
 
@@ -151,6 +158,9 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
                 "q and the caches must agree on batch and head count, got q=",
                 q.sizes(), " cache=", k_cache.sizes());
   }
+  TORCH_CHECK(q.size(3) == k_cache.size(3),
+              "q and the caches must have the same head_dim, got ", q.size(3), " and ",
+              k_cache.size(3));
   TORCH_CHECK(k_cache.size(2) > 0, "cache length must be > 0");
 
   TORCH_CHECK(seq_lens.is_cuda(), "seq_lens", " must be a CUDA tensor");
@@ -178,19 +188,20 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
   const int kv_heads = static_cast<int>(k_cache.size(1));
   const int max_seq = static_cast<int>(k_cache.size(2));
   const int split = static_cast<int>(split_size);
+  const int head_dim = static_cast<int>(q.size(3));
   const size_t ws_bytes =
-      fa_decode_gqa_workspace_bytes(batch, heads, kv_heads, max_seq, split);
+      fa_decode_hd_workspace_bytes(batch, heads, kv_heads, max_seq, head_dim, split);
   check_status(ws_bytes > 0 ? FA_OK : FA_ERR_INVALID_ARGUMENT);
   // Transient, stream-ordered workspace from the caching allocator
   // (decode.cu:215-219 of the reference).
   at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes / sizeof(float))},
                             q.options().dtype(at::kFloat));
-  check_status(fa_decode_gqa(q.const_data_ptr(), k_cache.const_data_ptr(),
-                             v_cache.const_data_ptr(),
-                             seq_lens.const_data_ptr<int32_t>(), o.data_ptr(),
-                             out_f32 ? FA_OUT_F32 : FA_OUT_F16, batch, heads, kv_heads,
-                             max_seq, static_cast<float>(scale), split,
-                             ws.data_ptr(), ws_bytes, stream_of(q)));
+  check_status(fa_decode_hd(q.const_data_ptr(), k_cache.const_data_ptr(),
+                            v_cache.const_data_ptr(),
+                            seq_lens.const_data_ptr<int32_t>(), o.data_ptr(),
+                            out_f32 ? FA_OUT_F32 : FA_OUT_F16, batch, heads, kv_heads,
+                            max_seq, head_dim, static_cast<float>(scale), split,
+                            ws.data_ptr(), ws_bytes, stream_of(q)));
   return o;
 }
 
@@ -244,9 +255,9 @@ void append_kv(const at::Tensor &k_cache, const at::Tensor &v_cache, const at::T
               "k_cache and v_cache must have identical shapes, got ", k_cache.sizes(), " and ",
               v_cache.sizes());
   TORCH_CHECK(k.size(2) == 1 && k.sizes() == v.sizes() && k.size(0) == k_cache.size(0) &&
-                  k.size(1) == k_cache.size(1),
-              "append_kv expects k and v of shape [B, H_kv, 1, 64] matching the caches, got k=",
-              k.sizes(), " v=", v.sizes(), " cache=", k_cache.sizes());
+                  k.size(1) == k_cache.size(1) && k.size(3) == k_cache.size(3),
+              "append_kv expects k and v of shape [B, H_kv, 1, head_dim] matching the caches, "
+              "got k=", k.sizes(), " v=", v.sizes(), " cache=", k_cache.sizes());
   TORCH_CHECK(k_cache.size(2) > 0, "cache length must be > 0");
   TORCH_CHECK(seq_lens.is_cuda(), "seq_lens", " must be a CUDA tensor");
   TORCH_CHECK(seq_lens.is_contiguous(), "seq_lens", " must be contiguous row-major");
@@ -259,10 +270,12 @@ void append_kv(const at::Tensor &k_cache, const at::Tensor &v_cache, const at::T
               "caches, k, v and seq_lens must live on the same device");
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(k_cache.device());
   if (k_cache.numel() == 0) return;
-  check_status(fa_kv_append(k_cache.data_ptr(), v_cache.data_ptr(), k.const_data_ptr(),
-                            v.const_data_ptr(), seq_lens.data_ptr<int32_t>(),
-                            static_cast<int>(k_cache.size(0)), static_cast<int>(k_cache.size(1)),
-                            static_cast<int>(k_cache.size(2)), stream_of(k_cache)));
+  check_status(fa_kv_append_hd(k_cache.data_ptr(), v_cache.data_ptr(), k.const_data_ptr(),
+                               v.const_data_ptr(), seq_lens.data_ptr<int32_t>(),
+                               static_cast<int>(k_cache.size(0)),
+                               static_cast<int>(k_cache.size(1)),
+                               static_cast<int>(k_cache.size(2)),
+                               static_cast<int>(k_cache.size(3)), stream_of(k_cache)));
 }
 
 // bindings.cpp:80-97.
@@ -337,6 +350,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Batched multi-head causal FlashAttention kernels for head_dim=64 "
             "(MI355X / gfx950)";
   m.attr("head_dim") = kHeadDim;
+  // Head sizes the kernels accept (128: no reference counterpart).
+  m.attr("head_dims") = py::make_tuple(kHeadDim, 128);
 
   m.def("prefill", &prefill,
         "Full-sequence attention (fp16 in/out, fp32 accum)", py::arg("q"),

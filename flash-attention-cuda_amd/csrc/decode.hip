@@ -53,10 +53,27 @@ namespace {
 
 constexpr int kSplitThreads = 256;  // 4 independent waves
 constexpr int kSplitWaves = kSplitThreads / kWave;
-constexpr int kRowsPerGroup = 8;    // rows covered by one wave load
 constexpr int kGroupsPerStep = 8;   // row groups loaded together per wave
-constexpr int kMergeThreads = kHeadDim;
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
+
+// Row geometry of the VALU kernels for head_dim D (64 or 128): a lane owns 8
+// head dims (16 B), D / 8 lanes cover one cache row, so one wave load moves
+// 512 / D rows (8 rows of 128 B, or 4 rows of 256 B).
+template <int D>
+struct RowGeo {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int kLanesPerRow = D / 8;
+  static constexpr int kRowsPerGroup = kWave / kLanesPerRow;
+};
+
+// Sum over each aligned group of D / 8 lanes (8 or 16); every lane gets the
+// group total.
+template <int D>
+__device__ __forceinline__ float sum_row_lanes(float x) {
+  x = sum_lanes8(x);
+  if constexpr (D == 128) x += dpp<kDppRowMirror>(x);
+  return x;
+}
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -74,15 +91,15 @@ struct RowSlotsT {
   uint4 v[G];
 };
 
-template <int G>
+template <int D, int G>
 __device__ __forceinline__ void load_slots(RowSlotsT<G> &r, const _Float16 *kp,
                                            const _Float16 *vp, int row0,
                                            int end, int sub, int slice) {
 #pragma unroll
   for (int u = 0; u < G; ++u) {
-    const int row = row0 + u * kRowsPerGroup + sub;
+    const int row = row0 + u * RowGeo<D>::kRowsPerGroup + sub;
     if (row < end) {
-      const size_t off = static_cast<size_t>(row) * kHeadDim + slice * 8;
+      const size_t off = static_cast<size_t>(row) * D + slice * 8;
       r.k[u] = load_stream(kp + off);
       r.v[u] = load_stream(vp + off);
     } else {
@@ -104,7 +121,7 @@ __device__ __forceinline__ void unpack8(const uint4 &raw, float f[8]) {
 // Fold one sub-step of rows (already loaded) into the running state. The
 // q.k partial of a lane is four v_dot2_f32_f16 on the raw fp16 pairs (exact
 // fp16 products, fp32 sums), scaled once by qscale = scale * log2(e).
-template <int G>
+template <int D, int G>
 __device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r, const half2 (&qh)[4],
                                               float qscale, int row0, int end, int sub,
                                               float &m, float &l, float (&acc)[8]) {
@@ -115,8 +132,8 @@ __device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r, const half2
     float part = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) part = __builtin_amdgcn_fdot2(qh[t], kh[t], part, false);
-    part = sum_lanes8(part);
-    const int row = row0 + u * kRowsPerGroup + sub;
+    part = sum_row_lanes<D>(part);
+    const int row = row0 + u * RowGeo<D>::kRowsPerGroup + sub;
     s[u] = (row < end) ? part * qscale : -INFINITY;
   }
   float mx = s[0];
@@ -145,9 +162,10 @@ __device__ __forceinline__ void consume_slots(const RowSlotsT<G> &r, const half2
 }
 
 // Head dims [8 * slice, +8) of query row bh, as fp16 pairs.
+template <int D>
 __device__ __forceinline__ void load_query(const _Float16 *q, size_t bh, int slice,
                                            half2 (&qh)[4]) {
-  const uint4 raw = *reinterpret_cast<const uint4 *>(q + bh * kHeadDim + slice * 8);
+  const uint4 raw = *reinterpret_cast<const uint4 *>(q + bh * D + slice * 8);
   const half2 *h = reinterpret_cast<const half2 *>(&raw);
 #pragma unroll
   for (int t = 0; t < 4; ++t) qh[t] = h[t];
@@ -185,12 +203,14 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
 
 // Pass 1 (decode.cu:50-138): one wave folds cache rows
 // [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
-// partial (m, l, acc[64]). Unit u = chunk_i * (B * H) + (b * H + h) is
-// handled by wave u % 4 of block u / 4.
+// partial (m, l, acc[D]). Unit u = chunk_i * (B * H) + (b * H + h) is
+// handled by wave u % 4 of block u / 4. With grouped queries (group > 1,
+// head_dim 128 only) query head bh reads cache head bh / group.
+template <int D>
 __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
-    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads,
+    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads, int group,
     int max_seq, int n_splits, int n_units, int chunk, float qscale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int unit = static_cast<int>(blockIdx.x) * kSplitWaves +
@@ -204,8 +224,8 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   const int bh = unit % n_bh;
   const int b = bh / heads;
 
-  const int sub = lane >> 3;   // row inside an 8-row group
-  const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
+  const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
+  const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
 
   // decode.cu:69-71: clamp to the cache capacity. A chunk past the sequence
   // end has no rows: it writes nothing, and the merge pass only reads the
@@ -215,19 +235,19 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   if (begin >= len) return;
   const int end = min(len, begin + chunk);
 
-  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const size_t head_off = static_cast<size_t>(bh / group) * max_seq * D;
   const _Float16 *kp = k_cache + head_off;
   const _Float16 *vp = v_cache + head_off;
 
   // Double-buffered row slots: the loads of sub-step i+1 are in flight while
   // sub-step i is consumed.
-  constexpr int kStepRows = kRowsPerGroup * kGroupsPerStep;
+  constexpr int kStepRows = RowGeo<D>::kRowsPerGroup * kGroupsPerStep;
   RowSlotsT<kGroupsPerStep> cur, nxt;
   int row0 = begin;
-  load_slots(cur, kp, vp, row0, end, sub, slice);
+  load_slots<D>(cur, kp, vp, row0, end, sub, slice);
 
   half2 qh[4];
-  load_query(q, bh, slice, qh);
+  load_query<D>(q, bh, slice, qh);
 
   float m = kNegBig, l = 0.f, acc[8];
 #pragma unroll
@@ -236,16 +256,16 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   for (;;) {
     const int next0 = row0 + kStepRows;
     const bool more = next0 < end;
-    if (more) load_slots(nxt, kp, vp, next0, end, sub, slice);
-    consume_slots(cur, qh, qscale, row0, end, sub, m, l, acc);
+    if (more) load_slots<D>(nxt, kp, vp, next0, end, sub, slice);
+    consume_slots<D>(cur, qh, qscale, row0, end, sub, m, l, acc);
     if (!more) break;
     cur = nxt;
     row0 = next0;
   }
 
-  // Merge the 8 row groups of the wave (lanes that share `slice`).
+  // Merge the row groups of the wave (lanes that share `slice`).
 #pragma unroll
-  for (int off = 8; off < kWave; off <<= 1) {
+  for (int off = RowGeo<D>::kLanesPerRow; off < kWave; off <<= 1) {
     const float mb = __shfl_xor(m, off);
     const float lb = __shfl_xor(l, off);
     float accb[8];
@@ -256,7 +276,7 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
 
   if (sub == 0) {
     const size_t slot = static_cast<size_t>(bh) * n_splits + split;
-    float4 *dst = reinterpret_cast<float4 *>(part_acc + slot * kHeadDim + slice * 8);
+    float4 *dst = reinterpret_cast<float4 *>(part_acc + slot * D + slice * 8);
     dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     if (slice == 0) *reinterpret_cast<float2 *>(part_ml + slot * 2) = make_float2(m, l);
@@ -283,26 +303,30 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-template <bool OUT_F32>
-__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+// D threads: lane = threadIdx.x % 64 runs the per-chunk statistics (each wave
+// of a 128-thread block computes them for itself), dim = threadIdx.x is the
+// head dim it accumulates.
+template <int D, bool OUT_F32>
+__global__ __launch_bounds__(D) void decode_merge_kernel(
     const float *__restrict__ part_acc, const float *__restrict__ part_ml,
     const int32_t *__restrict__ seq_lens, void *__restrict__ o, int heads,
     int max_seq, int n_splits, int chunk) {
   constexpr int kBatch = 8;  // chunks whose partial rows are loaded together
   const int bh = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int dim = threadIdx.x;
   const size_t base = static_cast<size_t>(bh) * n_splits;
   // Issued together, before the number of live chunks is known: seq_len, the
-  // (m, l) of chunk `lane` and head dim `lane` of the first kBatch partials
+  // (m, l) of chunk `lane` and head dim `dim` of the first kBatch partials
   // (slots past the live ones are read, all inside the workspace, and then
   // discarded by a select).
   const int raw_len = seq_lens[bh / heads];
   float2 ml = make_float2(kNegBig, 0.f);
   if (lane < n_splits) ml = *reinterpret_cast<const float2 *>(part_ml + (base + lane) * 2);
   float x[kBatch];
-  const float *col = part_acc + base * kHeadDim + lane;
+  const float *col = part_acc + base * D + dim;
 #pragma unroll
-  for (int u = 0; u < kBatch; ++u) x[u] = (u < n_splits) ? col[u * kHeadDim] : 0.f;
+  for (int u = 0; u < kBatch; ++u) x[u] = (u < n_splits) ? col[u * D] : 0.f;
 
   const int len = min(raw_len, max_seq);
   const int n_act = len > 0 ? (len + chunk - 1) / chunk : 0;
@@ -335,14 +359,14 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     }
     for (; t + kBatch <= cnt; t += kBatch) {
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) x[u] = col[(s0 + t + u) * kHeadDim];
+      for (int u = 0; u < kBatch; ++u) x[u] = col[(s0 + t + u) * D];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) acc = fmaf(x[u], __shfl(w, t + u), acc);
     }
-    for (; t < cnt; ++t) acc = fmaf(col[(s0 + t) * kHeadDim], __shfl(w, t), acc);
+    for (; t < cnt; ++t) acc = fmaf(col[(s0 + t) * D], __shfl(w, t), acc);
   }
   const float out = (l_all > 0.f) ? acc / l_all : 0.f;
-  const size_t idx = static_cast<size_t>(bh) * kHeadDim + lane;
+  const size_t idx = static_cast<size_t>(bh) * D + dim;
   if (OUT_F32) {
     static_cast<float *>(o)[idx] = out;
   } else {
@@ -619,15 +643,15 @@ constexpr int kBhGroups = 4;  // 32-row sub-steps
 constexpr int kRankMax = 256;   // ranking costs batch^2 / 512 LDS reads per thread
 constexpr int kBhWavesPerCu = 5;  // streaming waves per CU when the grid is resident
 
-template <bool OUT_F32>
+template <int D, bool OUT_F32>
 __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
-    void *__restrict__ o, int batch, int heads, int max_seq, int chunk,
+    void *__restrict__ o, int batch, int heads, int group, int max_seq, int chunk,
     int target_waves, float qscale) {
   __shared__ int s_len[kRankMax];
   __shared__ int s_order[kRankMax];
-  __shared__ float s_acc[kBhWaves][kHeadDim];
+  __shared__ float s_acc[kBhWaves][D];
   __shared__ float s_m[kBhWaves];
   __shared__ float s_l[kBhWaves];
 
@@ -674,9 +698,9 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   }
   chunk = min(chunk, max_seq);  // max_seq <= 2^27 (host check): 8 * chunk fits in int
 
-  const int sub = lane >> 3;   // row inside an 8-row group
-  const int slice = lane & 7;  // head dims [8 * slice, 8 * slice + 8)
-  const size_t head_off = static_cast<size_t>(bh) * max_seq * kHeadDim;
+  const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
+  const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
+  const size_t head_off = static_cast<size_t>(bh / group) * max_seq * D;
   const _Float16 *kp = k_cache + head_off;
   const _Float16 *vp = v_cache + head_off;
 
@@ -684,16 +708,16 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
-  constexpr int kStepRows = kRowsPerGroup * kBhGroups;  // 32
+  constexpr int kStepRows = RowGeo<D>::kRowsPerGroup * kBhGroups;  // 32 (D 64) / 16
   const int stride = kBhWaves * chunk;  // distance between a wave's chunks
   int c0 = wave * chunk;                // this wave's current chunk
   if (c0 < len) {
     half2 qh[4];
-    load_query(q, bh, slice, qh);
+    load_query<D>(q, bh, slice, qh);
     int end = min(len, c0 + chunk);
     int row0 = c0;
     RowSlotsT<kBhGroups> cur, nxt;
-    load_slots(cur, kp, vp, row0, end, sub, slice);
+    load_slots<D>(cur, kp, vp, row0, end, sub, slice);
     for (;;) {
       // Next sub-step: the rest of this chunk, else this wave's next chunk.
       int n_row0 = row0 + kStepRows, n_end = end, n_c0 = c0;
@@ -703,8 +727,8 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
         n_end = min(len, n_c0 + chunk);
       }
       const bool more = n_row0 < n_end;
-      if (more) load_slots(nxt, kp, vp, n_row0, n_end, sub, slice);
-      consume_slots(cur, qh, qscale, row0, end, sub, m, l, acc);
+      if (more) load_slots<D>(nxt, kp, vp, n_row0, n_end, sub, slice);
+      consume_slots<D>(cur, qh, qscale, row0, end, sub, m, l, acc);
       if (!more) break;
       cur = nxt;
       row0 = n_row0;
@@ -713,9 +737,9 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     }
   }
 
-  // Merge the 8 row groups of the wave (lanes that share `slice`).
+  // Merge the row groups of the wave (lanes that share `slice`).
 #pragma unroll
-  for (int off = 8; off < kWave; off <<= 1) {
+  for (int off = RowGeo<D>::kLanesPerRow; off < kWave; off <<= 1) {
     const float mb = __shfl_xor(m, off);
     const float lb = __shfl_xor(l, off);
     float accb[8];
@@ -732,7 +756,7 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     }
   }
   __syncthreads();
-  if (tid < kHeadDim) {
+  if (tid < D) {
     float mb = s_m[0];
 #pragma unroll
     for (int w = 1; w < kBhWaves; ++w) mb = fmaxf(mb, s_m[w]);
@@ -745,7 +769,7 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     }
     // decode.cu:172: a sequence with no rows gets a zero output.
     const float out = (lb > 0.f) ? ab / lb : 0.f;
-    const size_t idx = static_cast<size_t>(bh) * kHeadDim + tid;
+    const size_t idx = static_cast<size_t>(bh) * D + tid;
     if (OUT_F32)
       static_cast<float *>(o)[idx] = out;
     else
@@ -753,7 +777,8 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   }
 }
 
-// Blocks of decode_bh_kernel resident on one CU at once, per device.
+// Blocks of decode_bh_kernel<D> resident on one CU at once, per device.
+template <int D>
 int bh_blocks_per_cu(int device) {
   static std::once_flag once[kMaxDevices];
   static int blocks[kMaxDevices];
@@ -764,7 +789,7 @@ int bh_blocks_per_cu(int device) {
     if (hipGetDevice(&prev) != hipSuccess) return;
     if (hipSetDevice(device) == hipSuccess &&
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void *>(decode_bh_kernel<false>), kBhThreads, 0) !=
+            &n, reinterpret_cast<const void *>(decode_bh_kernel<D, false>), kBhThreads, 0) !=
             hipSuccess)
       n = 0;
     (void)hipSetDevice(prev);
@@ -821,11 +846,80 @@ int decode_group_chunk(int batch, int units_per_row, int max_seq) {
   return static_cast<int>(std::min(rows, std::max<long long>(cap, 2 * kGroupTile)));
 }
 
+namespace {
+
+// The VALU kernels for head_dim D: the whole-sequence kernel when B * H fills
+// the chip (or the cache is short), else split-K and the merge. group > 1
+// (head_dim 128 only) makes query head bh read K/V head bh / group.
+template <int D>
+int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
+                       const int32_t *seq_lens, void *o, bool out_f32, int batch, int heads,
+                       int group, int max_seq, float scale, int split_size, bool auto_split,
+                       float *workspace, hipStream_t stream) {
+  const int n_splits = (max_seq + split_size - 1) / split_size;
+  const size_t bh = static_cast<size_t>(batch) * heads;
+  if (use_bh_path(batch, heads, max_seq)) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != FA_OK) return rc;
+    const int cu = device_cu_count(dev);
+    const bool resident = bh <= static_cast<size_t>(bh_blocks_per_cu<D>(dev)) * cu;
+    const int target_waves = resident ? kBhWavesPerCu * cu : 0;
+    if (out_f32)
+      hipLaunchKernelGGL((decode_bh_kernel<D, true>), dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, group, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
+    else
+      hipLaunchKernelGGL((decode_bh_kernel<D, false>), dim3(static_cast<unsigned>(bh)),
+                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
+                         static_cast<const _Float16 *>(k_cache),
+                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
+                         heads, group, max_seq, auto_split ? 0 : split_size,
+                         target_waves, scale * kLog2e);
+    return check_hip(hipGetLastError(), "decode_bh_kernel launch");
+  }
+  float *part_acc = workspace;
+  float *part_ml = workspace + bh * n_splits * D;
+  const size_t n_units = bh * n_splits;
+  const unsigned split_blocks =
+      static_cast<unsigned>((n_units + kSplitWaves - 1) / kSplitWaves);
+
+  hipLaunchKernelGGL((decode_split_kernel<D>), dim3(split_blocks),
+                     dim3(kSplitThreads), 0, stream,
+                     static_cast<const _Float16 *>(q),
+                     static_cast<const _Float16 *>(k_cache),
+                     static_cast<const _Float16 *>(v_cache), seq_lens,
+                     part_acc, part_ml, heads, group, max_seq, n_splits,
+                     static_cast<int>(n_units), split_size, scale * kLog2e);
+  int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
+  if (rc != FA_OK) return rc;
+
+  if (out_f32) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, true>), dim3(static_cast<unsigned>(bh)),
+                       dim3(D), 0, stream, part_acc, part_ml, seq_lens,
+                       o, heads, max_seq, n_splits, split_size);
+  } else {
+    hipLaunchKernelGGL((decode_merge_kernel<D, false>), dim3(static_cast<unsigned>(bh)),
+                       dim3(D), 0, stream, part_acc, part_ml, seq_lens,
+                       o, heads, max_seq, n_splits, split_size);
+  }
+  return check_hip(hipGetLastError(), "decode_merge_kernel launch");
+}
+
+}  // namespace
+
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
-                  int heads, int kv_heads, int max_seq, float scale, int split_size,
-                  bool auto_split, float *workspace, hipStream_t stream) {
+                  int heads, int kv_heads, int max_seq, int head_dim, float scale,
+                  int split_size, bool auto_split, float *workspace, hipStream_t stream) {
   const int group = heads / kv_heads;
+  if (head_dim == 128)
+    return launch_valu_decode<128>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads,
+                                   group, max_seq, scale, split_size, auto_split, workspace,
+                                   stream);
   if (group > 1) {
     // Grouped queries: the matrix-core split pass, then the common merge.
     const int nqg = group_queries(group);
@@ -844,76 +938,33 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
     if (rc != FA_OK) return rc;
     const unsigned n_bh = static_cast<unsigned>(static_cast<size_t>(batch) * heads);
     if (out_f32)
-      hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(n_bh), dim3(kMergeThreads), 0, stream,
+      hipLaunchKernelGGL((decode_merge_kernel<64, true>), dim3(n_bh), dim3(kHeadDim), 0, stream,
                          part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
     else
-      hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(n_bh), dim3(kMergeThreads), 0, stream,
+      hipLaunchKernelGGL((decode_merge_kernel<64, false>), dim3(n_bh), dim3(kHeadDim), 0, stream,
                          part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
     return check_hip(hipGetLastError(), "decode_merge_kernel launch");
   }
-  const int n_splits = (max_seq + split_size - 1) / split_size;
-  const size_t bh = static_cast<size_t>(batch) * heads;
-  if (use_bh_path(batch, heads, max_seq)) {
-    int dev = 0;
-    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
-    if (rc != FA_OK) return rc;
-    const int cu = device_cu_count(dev);
-    const bool resident = bh <= static_cast<size_t>(bh_blocks_per_cu(dev)) * cu;
-    const int target_waves = resident ? kBhWavesPerCu * cu : 0;
-    if (out_f32)
-      hipLaunchKernelGGL(decode_bh_kernel<true>, dim3(static_cast<unsigned>(bh)),
-                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
-                         static_cast<const _Float16 *>(k_cache),
-                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
-                         heads, max_seq, auto_split ? 0 : split_size,
-                         target_waves, scale * kLog2e);
-    else
-      hipLaunchKernelGGL(decode_bh_kernel<false>, dim3(static_cast<unsigned>(bh)),
-                         dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
-                         static_cast<const _Float16 *>(k_cache),
-                         static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
-                         heads, max_seq, auto_split ? 0 : split_size,
-                         target_waves, scale * kLog2e);
-    return check_hip(hipGetLastError(), "decode_bh_kernel launch");
-  }
-  float *part_acc = workspace;
-  float *part_ml = workspace + bh * n_splits * kHeadDim;
-  const size_t n_units = bh * n_splits;
-  const unsigned split_blocks =
-      static_cast<unsigned>((n_units + kSplitWaves - 1) / kSplitWaves);
-
-  hipLaunchKernelGGL(decode_split_kernel, dim3(split_blocks),
-                     dim3(kSplitThreads), 0, stream,
-                     static_cast<const _Float16 *>(q),
-                     static_cast<const _Float16 *>(k_cache),
-                     static_cast<const _Float16 *>(v_cache), seq_lens,
-                     part_acc, part_ml, heads, max_seq, n_splits,
-                     static_cast<int>(n_units), split_size, scale * kLog2e);
-  int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
-  if (rc != FA_OK) return rc;
-
-  if (out_f32) {
-    hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(static_cast<unsigned>(bh)),
-                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, seq_lens,
-                       o, heads, max_seq, n_splits, split_size);
-  } else {
-    hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(static_cast<unsigned>(bh)),
-                       dim3(kMergeThreads), 0, stream, part_acc, part_ml, seq_lens,
-                       o, heads, max_seq, n_splits, split_size);
-  }
-  return check_hip(hipGetLastError(), "decode_merge_kernel launch");
+  return launch_valu_decode<64>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads, 1,
+                                max_seq, scale, split_size, auto_split, workspace, stream);
 }
 
 int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
   struct K { const char *name; const void *fn; int threads; };
   const K ks[] = {
-      {"decode_split_kernel", reinterpret_cast<const void *>(decode_split_kernel),
+      {"decode_split_kernel", reinterpret_cast<const void *>(decode_split_kernel<64>),
        kSplitThreads},
       {"decode_merge_kernel",
-       reinterpret_cast<const void *>(decode_merge_kernel<false>), kMergeThreads},
-      {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<false>),
+       reinterpret_cast<const void *>(decode_merge_kernel<64, false>), kHeadDim},
+      {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<64, false>),
        kBhThreads},
       {"decode_group_kernel", reinterpret_cast<const void *>(decode_group_kernel), kWave},
+      {"decode_split_kernel<head_dim=128>",
+       reinterpret_cast<const void *>(decode_split_kernel<128>), kSplitThreads},
+      {"decode_merge_kernel<head_dim=128>",
+       reinterpret_cast<const void *>(decode_merge_kernel<128, false>), 128},
+      {"decode_bh_kernel<head_dim=128>",
+       reinterpret_cast<const void *>(decode_bh_kernel<128, false>), kBhThreads},
   };
   for (const K &k : ks) {
     if (*n < cap) {

@@ -37,13 +37,16 @@ int device_cu_count(int device);
 
 // ---- kernel launchers (prefill.hip / decode.hip) ---------------------------
 // kv_heads divides heads; query head h reads K/V head h / (heads / kv_heads).
+// head_dim is 64 or 128.
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
                    bool out_f32, int batch, int heads, int kv_heads, int seq,
-                   bool causal, float scale, hipStream_t stream);
+                   int head_dim, bool causal, float scale, hipStream_t stream);
+// head_dim is 64 or 128; grouped queries at head_dim 128 take the VALU
+// split-K / whole-sequence kernels with K/V head bh / group.
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
-                  int heads, int kv_heads, int max_seq, float scale, int split_size,
-                  bool auto_split, float *workspace, hipStream_t stream);
+                  int heads, int kv_heads, int max_seq, int head_dim, float scale,
+                  int split_size, bool auto_split, float *workspace, hipStream_t stream);
 // Decode work units per batch row: one per head without grouped queries,
 // else one per (K/V head, chunk of up to 32 of its query heads).
 int decode_units_per_row(int heads, int kv_heads);
@@ -55,7 +58,7 @@ int decode_group_chunk(int batch, int units_per_row, int max_seq);
 // Writes k_new / v_new ([B, H_kv, 1, 64]) at row seq_lens[b] of the caches
 // and advances seq_lens[b] (kv_cache.hip).
 int launch_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
-                     int32_t *seq_lens, int batch, int kv_heads, int max_seq,
+                     int32_t *seq_lens, int batch, int kv_heads, int max_seq, int head_dim,
                      hipStream_t stream);
 
 // o = softmax(q k^T / 8) v for one (n, 64) fp32 head, no mask; variant is an
@@ -81,6 +84,7 @@ __device__ __forceinline__ float dpp(float x) {
 constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i inside 8 lanes
+constexpr int kDppRowMirror = 0x140;  // lane i <-> 15 - i inside 16 lanes
 
 // Sum over each aligned group of 8 lanes; every lane gets the group total.
 __device__ __forceinline__ float sum_lanes8(float x) {

@@ -1,6 +1,6 @@
 // MFMA tile building blocks shared by the gfx950 attention kernels
 // (prefill.hip, decode.hip): the 16-byte-chunk swizzles of a row-major
-// [rows x 64] fp16 tile in LDS, direct global->LDS loads, the fragment
+// [rows x 64] (or [rows x 128]) fp16 tile in LDS, direct global->LDS loads, the fragment
 // offsets of v_mfma_f32_32x32x16_f16 operands read from such a tile, and the
 // lane-pair max of an S^T accumulator.
 //
@@ -94,6 +94,53 @@ __device__ __forceinline__ FragOffsets frag_offsets(int lane) {
   for (int db = 0; db < 2; ++db) {
     const int d = db * 32 + tr_dim;
     f.v[db] = tr_row * kHeadDim + (((d >> 3) ^ v_swz(tr_row)) << 3) + (d & 7);
+  }
+  return f;
+}
+
+// The same building blocks for tiles of D-dim rows, D in {64, 128}. D = 64 is
+// exactly the layout above. D = 128 rows are 256 B (16 chunks), so a row
+// no longer shifts the bank group of a chunk and the swizzles change:
+//  K, Q: a ds_read_b128 phase reads one logical chunk of 8 or 16
+//     consecutive rows; chunk c of row r goes to position c ^ (r & 15),
+//     16 distinct positions for any 16 consecutive rows.
+//  V: a 32-lane transpose-read phase reads chunks {4 db, .., 4 db + 3} of 4
+//     consecutive rows; c ^ 4 (r & 3) maps those 16 (row, chunk) pairs to 16
+//     distinct positions.
+// Fragment order for Q/K: k-step s, lane half g holds chunk (D / 16) g + s
+// (head dims [(D / 2) g + 8 s, +8)); A and B use the same order.
+template <int D>
+__device__ __forceinline__ int k_swz_d(int row) {
+  if constexpr (D == 64) return k_swz(row);
+  else return row & 15;
+}
+template <int D>
+__device__ __forceinline__ int v_swz_d(int row) {
+  if constexpr (D == 64) return v_swz(row);
+  else return (row & 3) << 2;
+}
+
+template <int D>
+struct FragOffsetsD {
+  int k[D / 16];  // K (and Q) fragment for d-step s (key block 0; block 1 is +32 rows)
+  int v[D / 32];  // V^T transpose-read base for d-block db
+};
+
+template <int D>
+__device__ __forceinline__ FragOffsetsD<D> frag_offsets_d(int lane) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  FragOffsetsD<D> f;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s)
+    f.k[s] = col * D + ((((D / 16) * g + s) ^ k_swz_d<D>(col)) << 3);
+  const int tr_row = 4 * g + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+    const int d = db * 32 + tr_dim;
+    f.v[db] = tr_row * D + (((d >> 3) ^ v_swz_d<D>(tr_row)) << 3) + (d & 7);
   }
   return f;
 }

@@ -86,8 +86,6 @@ constexpr int kWaves = 2 * kRowWaves;         // x 2 key halves
 constexpr int kThreads = kWaves * kWave;      // 512
 constexpr int kRowsPerWave = 32;
 constexpr int kBr = kRowWaves * kRowsPerWave; // 128 query rows per block
-constexpr int kBc = 64;                       // keys per tile
-constexpr int kTileHalves = kBc * kHeadDim;   // 4096 halves = 8 KiB
 constexpr int kKStages = 4;
 constexpr int kVStages = 5;
 constexpr int kAhead = 4;                     // tiles in flight ahead of use
@@ -95,51 +93,78 @@ constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per 
 constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split P
 constexpr float kNegHuge = -3.0e38f;
 
-// LDS (halves): [Q: 128 rows x 64] [half 0: K ring | V ring] [half 1: ...]
-constexpr int kQHalves = kBr * kHeadDim;                         // 16 KiB
-constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
-constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 KiB
+// Tile geometry for head_dim D (64 or 128). A K or V tile is always 8 KiB:
+// 64 keys of 128 B rows for D = 64, 32 keys of 256 B rows for D = 128, so a
+// step is 16 MFMAs either way (D = 64: QK 2 key blocks x 4 d-steps, PV 4
+// k-steps x 2 d-blocks; D = 128: QK 1 x 8, PV 2 x 4).
+template <int D>
+struct Geo {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int kBc = D == 64 ? 64 : 32;    // keys per tile
+  static constexpr int kKB = kBc / 32;             // 32-key blocks per tile (S^T tiles)
+  static constexpr int kDS = D / 16;               // k-steps of S^T = K Q^T
+  static constexpr int kDB = D / 32;               // d-blocks of O^T
+  static constexpr int kKS = kBc / 16;             // k-steps of O^T += V^T P^T
+  static constexpr int kChunks = D / 8;            // 16-byte chunks per row
+  static constexpr int kRowsPerLoad = kWave / kChunks;  // rows per wave load
+  static constexpr int kTileHalves = kBc * D;      // 4096 halves = 8 KiB
+  // D = 64 stages the Q tile in LDS; D = 128 loads Q^T straight into
+  // registers, which leaves the whole LDS to the two rings.
+  static constexpr bool kQInLds = D == 64;
+  // LDS (halves): [Q: 128 rows x 64 (D = 64 only)] [half 0: K ring | V ring] [half 1: ...]
+  static constexpr int kQHalves = kQInLds ? kBr * D : 0;                  // 16 KiB / 0
+  static constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
+  static constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 / 144 KiB
+  // Half-merge exchange at the end: [row wave][O^T values, m, l][64 lanes] fp32.
+  static constexpr int kXchg = 16 * kDB + 2;
+  static_assert(kRowWaves * kXchg * kWave * 4 <= kLdsHalves * 2, "exchange fits in LDS");
+};
 
 
 __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
   return *reinterpret_cast<const half8 *>(p);
 }
 
+template <int D>
 struct SoftmaxState {
-  float m;       // running max (log2 domain, already scaled by c)
-  float l;       // this lane's share of the row sum
-  floatx16 o[2]; // O^T accumulators: d-blocks 0 and 1
+  float m;                      // running max (log2 domain, already scaled by c)
+  float l;                      // this lane's share of the row sum
+  floatx16 o[Geo<D>::kDB];      // O^T accumulators, one per 32-dim block
 };
 
 // Register copies of the LDS fragments one tile step consumes.
-struct KFrags { half8 f[2][4]; };  // [32-key block][d-step]
-struct VFrags { half8 f[4][2]; };  // [16-key step][d-block]
+template <int D>
+struct KFrags { half8 f[Geo<D>::kKB][Geo<D>::kDS]; };  // [32-key block][d-step]
+template <int D>
+struct VFrags { half8 f[Geo<D>::kKS][Geo<D>::kDB]; };  // [16-key step][d-block]
 
 
+template <int D>
 __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
-                                       const FragOffsets &fo, KFrags &k) {
+                                       const FragOffsetsD<D> &fo, KFrags<D> &k) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < Geo<D>::kDS; ++s) {
     lds_half *p = opaque_lds(tile + fo.k[s]);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < Geo<D>::kKB; ++kb)
       k.f[kb][s] = *reinterpret_cast<__attribute__((address_space(3))) const half8 *>(
-          p + kb * 32 * kHeadDim);
+          p + kb * 32 * D);
   }
 }
 
+template <int D>
 __device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
-                                       const FragOffsets &fo, VFrags &v) {
+                                       const FragOffsetsD<D> &fo, VFrags<D> &v) {
 #pragma unroll
-  for (int db = 0; db < 2; ++db) {
+  for (int db = 0; db < Geo<D>::kDB; ++db) {
     lds_half *p = opaque_lds(tile + fo.v[db]);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < Geo<D>::kKS; ++ks) {
       const int kb = ks >> 1, h = ks & 1;
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
         const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) short4v *)(p + (kb * 32 + 16 * h + 8 * part) * kHeadDim));
+            (__attribute__((address_space(3))) short4v *)(p + (kb * 32 + 16 * h + 8 * part) * D));
         const half4 v4 = __builtin_bit_cast(half4, r);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v.f[ks][db][4 * part + e] = v4[e];
@@ -148,37 +173,39 @@ __device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
   }
 }
 
-// S^T[kb] = K_kb Q^T for both 32-key blocks (8 MFMAs, two chains).
-__device__ __forceinline__ void qk_mfma(const KFrags &k, const half8 (&qf)[4],
-                                        floatx16 (&s)[2]) {
+// S^T[kb] = K_kb Q^T for every 32-key block of the tile (8 MFMAs).
+template <int D>
+__device__ __forceinline__ void qk_mfma(const KFrags<D> &k, const half8 (&qf)[Geo<D>::kDS],
+                                        floatx16 (&s)[Geo<D>::kKB]) {
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < Geo<D>::kKB; ++kb)
 #pragma unroll
     for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < Geo<D>::kDS; ++i)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
+    for (int kb = 0; kb < Geo<D>::kKB; ++kb) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
 }
 
-// O^T[db] += V^T_db P^T (8 MFMAs, two chains).
-__device__ __forceinline__ void pv_mfma(const VFrags &v, const half8 (&p)[4],
-                                        floatx16 (&o)[2]) {
+// O^T[db] += V^T_db P^T for every 32-dim block (8 MFMAs).
+template <int D>
+__device__ __forceinline__ void pv_mfma(const VFrags<D> &v, const half8 (&p)[Geo<D>::kKS],
+                                        floatx16 (&o)[Geo<D>::kDB]) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < Geo<D>::kKS; ++ks)
 #pragma unroll
-    for (int db = 0; db < 2; ++db) o[db] = mfma(v.f[ks][db], p[ks], o[db]);
+    for (int db = 0; db < Geo<D>::kDB; ++db) o[db] = mfma(v.f[ks][db], p[ks], o[db]);
 }
 
 // New running max for one tile; returns alpha, the factor that rescales the
 // previous O and l (l is rescaled here, O by the caller).
 // MASK: keys past the end or above the causal diagonal become -inf.
-template <bool CAUSAL, bool MASK>
-__device__ __forceinline__ float tile_max(floatx16 (&s)[2], int lim, float c_scale,
-                                          SoftmaxState &st) {
+template <bool CAUSAL, bool MASK, int D>
+__device__ __forceinline__ float tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, float c_scale,
+                                          SoftmaxState<D> &st) {
   float mx = -INFINITY;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < Geo<D>::kKB; ++kb) {
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       if (MASK)
@@ -195,15 +222,15 @@ __device__ __forceinline__ float tile_max(floatx16 (&s)[2], int lim, float c_sca
 }
 
 // P^T fragments (hi [+ lo]) of one tile and the row-sum update.
-template <bool MASK, bool SPLIT>
-__device__ __forceinline__ void tile_exp(const floatx16 (&s)[2], float c_scale,
-                                         SoftmaxState &st, half8 (&p_hi)[4],
-                                         half8 (&p_lo)[4]) {
+template <bool MASK, bool SPLIT, int D>
+__device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float c_scale,
+                                         SoftmaxState<D> &st, half8 (&p_hi)[Geo<D>::kKS],
+                                         half8 (&p_lo)[Geo<D>::kKS]) {
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   const float m_use = st.m;
   float lsum = 0.f;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < Geo<D>::kKS; ++ks) {
     const int kb = ks >> 1, h = ks & 1;
 #pragma unroll
     for (int t = 0; t < 8; t += 2) {
@@ -232,10 +259,11 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[2], float c_scale,
 
 // O *= alpha when the max of any row of the wave rose (wave-uniform branch;
 // alpha is exactly 1 otherwise).
-__device__ __forceinline__ void rescale_o(SoftmaxState &st, float alpha) {
+template <int D>
+__device__ __forceinline__ void rescale_o(SoftmaxState<D> &st, float alpha) {
   if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < Geo<D>::kDB; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a) st.o[db][a] *= alpha;
   }
@@ -256,34 +284,37 @@ __device__ __forceinline__ void interleave_step() {
 // Pins the P fragments of a step to that step: without a use there, the
 // compiler sinks their computation into the next step (next to the PV MFMAs
 // that consume them), which defeats the interleave.
-__device__ __forceinline__ void keep(const half8 (&p)[4]) {
+template <int N>
+__device__ __forceinline__ void keep(const half8 (&p)[N]) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(p[ks]));
+  for (int ks = 0; ks < N; ++ks) asm volatile("" ::"v"(p[ks]));
 }
 
 // Plain (non-pipelined) step for masked / short-row tiles: QK, softmax with
 // mask and split P, PV issued twice.
-template <bool CAUSAL>
-__device__ __forceinline__ void slow_step(const KFrags &kf, const VFrags &vf,
-                                          const half8 (&qf)[4], int key0, int seq,
+template <bool CAUSAL, int D>
+__device__ __forceinline__ void slow_step(const KFrags<D> &kf, const VFrags<D> &vf,
+                                          const half8 (&qf)[Geo<D>::kDS], int key0, int seq,
                                           int my_q, int lane, float c_scale,
-                                          SoftmaxState &st) {
-  floatx16 s[2];
-  qk_mfma(kf, qf, s);
+                                          SoftmaxState<D> &st) {
+  floatx16 s[Geo<D>::kKB];
+  qk_mfma<D>(kf, qf, s);
   // Element a of key block kb holds key key0 + kb*32 + 8 (a/4) + 4 g + a%4;
   // it is visible iff that offset is <= lim (last visible key - key0 - 4 g).
   const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
-  const float alpha = tile_max<CAUSAL, true>(s, lim, c_scale, st);
+  const float alpha = tile_max<CAUSAL, true, D>(s, lim, c_scale, st);
   rescale_o(st, alpha);
-  half8 p_hi[4], p_lo[4];
-  tile_exp<true, true>(s, c_scale, st, p_hi, p_lo);
-  pv_mfma(vf, p_hi, st.o);
-  pv_mfma(vf, p_lo, st.o);
+  half8 p_hi[Geo<D>::kKS], p_lo[Geo<D>::kKS];
+  tile_exp<true, true, D>(s, c_scale, st, p_hi, p_lo);
+  pv_mfma<D>(vf, p_hi, st.o);
+  pv_mfma<D>(vf, p_lo, st.o);
 }
 
 // The K and V rings of one key half: half h owns tiles 2 k + h (k = 0, 1,
 // ...), in K stage k % kKStages and V stage k % kVStages.
+template <int D>
 struct HalfRing {
+  using G = Geo<D>;
   _Float16 *kring, *vring;
   const _Float16 *kp, *vp;
   int seq, n_tiles, half;
@@ -294,23 +325,24 @@ struct HalfRing {
   __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
   __device__ __forceinline__ bool exists(int k) const { return tile(k) < n_tiles; }
   __device__ __forceinline__ _Float16 *kstage(int k) const {
-    return kring + (k % kKStages) * kTileHalves;
+    return kring + (k % kKStages) * G::kTileHalves;
   }
   __device__ __forceinline__ _Float16 *vstage(int k) const {
-    return vring + (k % kVStages) * kTileHalves;
+    return vring + (k % kVStages) * G::kTileHalves;
   }
-  // The half's four waves each load row blocks {2 wh, 2 wh + 1} (8 rows of
-  // 128 B each) of K and of V; lane = 8 * (row in block) + chunk. Rows past
-  // the sequence end are clamped to the last row: they are masked in the
-  // softmax (K) and weighted by 0 (V).
+  // The half's four waves each load row blocks {2 wh, 2 wh + 1} (one wave
+  // load each: 8 rows of 128 B for D = 64, 4 rows of 256 B for D = 128) of K
+  // and of V; lane = (D / 8) * (row in block) + chunk. Rows past the sequence
+  // end are clamped to the last row: they are masked in the softmax (K) and
+  // weighted by 0 (V).
   __device__ __forceinline__ void issue(int k) const {
     if (!exists(k)) return;
-    const int key0 = tile(k) * kBc;
+    const int key0 = tile(k) * G::kBc;
     _Float16 *const ks = kstage(k);
     _Float16 *const vs = vstage(k);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * kHeadDim;
+      const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * D;
       global_to_lds16(kp + row + src_off[0][i], ks + lds_off[i]);
       global_to_lds16(vp + row + src_off[1][i], vs + lds_off[i]);
     }
@@ -376,12 +408,18 @@ __device__ __forceinline__ int grouped_head(int h, int n_bh) {
   return start + (h >> 3);
 }
 
-template <bool CAUSAL, bool OUT_F32>
+template <int D, bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
     int n_qtiles, int group, float c_scale, bool negate_q) {
-  __shared__ __attribute__((aligned(1024))) _Float16 lds[kLdsHalves];
+  using G = Geo<D>;
+  constexpr int kBc = G::kBc;
+  constexpr int kKB = G::kKB;
+  constexpr int kKS = G::kKS;
+  constexpr int kDB = G::kDB;
+  constexpr int kDS = G::kDS;
+  __shared__ __attribute__((aligned(1024))) _Float16 lds[G::kLdsHalves];
 
   // Heaviest (last) query tiles first: one block fills a CU, so dispatching
   // in decreasing work order is a longest-first list schedule.
@@ -400,19 +438,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
   // Q and O are [B, H, S, 64], K and V [B, H / group, S, 64]: query head
   // b * H + h reads K/V head b * H / group + h / group = bh / group.
-  const size_t head_off = static_cast<size_t>(bh) * seq * kHeadDim;
-  const size_t kv_off = static_cast<size_t>(bh / group) * seq * kHeadDim;
+  const size_t head_off = static_cast<size_t>(bh) * seq * D;
+  const size_t kv_off = static_cast<size_t>(bh / group) * seq * D;
   const int q0 = qtile * kBr;
   const int qw0 = q0 + rw * kRowsPerWave;
   const int my_q = qw0 + col;
 
   const int key_end = CAUSAL ? min(seq, q0 + kBr) : seq;
   const int n_tiles = (key_end + kBc - 1) / kBc;
-  _Float16 *const half_lds = lds + kQHalves + half * kHalfHalves;
+  _Float16 *const half_lds = lds + G::kQHalves + half * G::kHalfHalves;
   _Float16 *const q_lds = lds;
-  HalfRing ring;
+  HalfRing<D> ring;
   ring.kring = half_lds;
-  ring.vring = half_lds + kKStages * kTileHalves;
+  ring.vring = half_lds + kKStages * G::kTileHalves;
   ring.kp = k + kv_off;
   ring.vp = v + kv_off;
   ring.seq = seq;
@@ -421,12 +459,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int rblock = 2 * rw + i;
-    const int r = rblock * 8 + (lane >> 3);
-    const int p = lane & 7;
+    const int r = rblock * G::kRowsPerLoad + lane / G::kChunks;
+    const int p = lane % G::kChunks;
     ring.row_in_tile[i] = r;
-    ring.src_off[0][i] = (p ^ k_swz(r)) << 3;
-    ring.src_off[1][i] = (p ^ v_swz(r)) << 3;
-    ring.lds_off[i] = rblock * 8 * kHeadDim;
+    ring.src_off[0][i] = (p ^ k_swz_d<D>(r)) << 3;
+    ring.src_off[1][i] = (p ^ v_swz_d<D>(r)) << 3;
+    ring.lds_off[i] = rblock * G::kRowsPerLoad * D;
   }
   const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
   // Tiles [0, 2 n_main) need no mask for any row of the block, and all its
@@ -440,16 +478,27 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
 
-  // Q tile (16 row blocks of 8 rows, 2 per wave; K swizzle), then this
-  // half's first kAhead tiles.
+  // Q: for D = 64 the tile goes to LDS (16 row blocks of 8 rows, 2 per wave;
+  // K swizzle); for D = 128 each lane loads its Q^T fragments (query my_q,
+  // head dims [64 g + 8 s, +8)) straight into registers. Then this half's
+  // first kAhead tiles.
+  const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
+  half8 qf[kDS];
+  if constexpr (G::kQInLds) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rblock = 2 * wave + i;
-    const int r = rblock * 8 + (lane >> 3);
-    const int row = min(q0 + r, seq - 1);
-    global_to_lds16(q + head_off + static_cast<size_t>(row) * kHeadDim +
-                        (((lane & 7) ^ k_swz(r)) << 3),
-                    q_lds + rblock * 8 * kHeadDim);
+    for (int i = 0; i < 2; ++i) {
+      const int rblock = 2 * wave + i;
+      const int r = rblock * 8 + (lane >> 3);
+      const int row = min(q0 + r, seq - 1);
+      global_to_lds16(q + head_off + static_cast<size_t>(row) * D +
+                          (((lane & 7) ^ k_swz(r)) << 3),
+                      q_lds + rblock * 8 * D);
+    }
+  } else {
+    const _Float16 *qrow = q + head_off + static_cast<size_t>(min(my_q, seq - 1)) * D +
+                           (lane >> 5) * (D / 2);
+#pragma unroll
+    for (int s = 0; s < kDS; ++s) qf[s] = *reinterpret_cast<const half8 *>(qrow + 8 * s);
   }
 #pragma unroll
   for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
@@ -463,20 +512,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     wait_loads<0>();
   __builtin_amdgcn_s_barrier();
 
-  const FragOffsets fo = frag_offsets(lane);
-  // Q^T fragments: lane holds query my_q, head dims [32 g + 8 s, +8).
-  half8 qf[4];
+  // Q^T fragments: lane holds query my_q, head dims [(D / 2) g + 8 s, +8).
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    qf[s] = lds_b128(q_lds + rw * kRowsPerWave * kHeadDim + fo.k[s]);
+  for (int s = 0; s < kDS; ++s) {
+    if constexpr (G::kQInLds) qf[s] = lds_b128(q_lds + rw * kRowsPerWave * D + fo.k[s]);
     if (negate_q) qf[s] = -qf[s];
   }
 
-  SoftmaxState st;
+  SoftmaxState<D> st;
   st.m = kNegHuge;
   st.l = 0.f;
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+  for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int a = 0; a < 16; ++a) st.o[db][a] = 0.f;
 
@@ -488,10 +535,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // and the result is discarded.
   int kk = 0;
   if (n_main > 0) {
-    floatx16 s_a[2], s_b[2];
-    half8 p_a[4], p_b[4], p_unused[4];
-    KFrags kf;
-    VFrags vf;
+    floatx16 s_a[kKB], s_b[kKB];
+    half8 p_a[kKS], p_b[kKS], p_unused[kKS];
+    KFrags<D> kf;
+    VFrags<D> vf;
     float alpha;
     read_k(ring.kstage(0), fo, kf);
     qk_mfma(kf, qf, s_a);
@@ -537,7 +584,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // masked softmax on the S that the previous step's QK produced; waves
     // that see none of that tile only drain. (Its P is not split: every row
     // of the block sees >= kSplitPRowsBelow keys.)
-    const bool tail = n_steps == n_main + 1;
+    // (head_dim 128: its 32-key tiles put two masked tiles in each half's
+    // range; the second one takes the plain step below.)
+    const bool tail = n_steps >= n_main + 1;
     if (kk < n_main) {  // one more (odd) main step; leaves S_{kk+1} in s_b, P_kk in p_a
       ring.advance(kk);
       rescale_o(st, alpha);
@@ -548,7 +597,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       read_v(ring.vstage(kk), fo, vf);
       ++kk;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) s_b[kb] = s_a[kb];
+      for (int kb = 0; kb < kKB; ++kb) s_b[kb] = s_a[kb];
     }
     if (tail) {
       ring.advance(kk);
@@ -578,15 +627,15 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   for (; kk < n_steps; ++kk) {
     const int key0 = ring.tile(kk) * kBc;
     const bool active = key0 < wave_key_end;
-    KFrags kf;
-    VFrags vf;
+    KFrags<D> kf;
+    VFrags<D> vf;
     if (active) {
       read_k(ring.kstage(kk), fo, kf);
       read_v(ring.vstage(kk), fo, vf);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done
     ring.advance(kk);
-    if (active) slow_step<CAUSAL>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
+    if (active) slow_step<CAUSAL, D>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
   }
 
   // ---- merge the two halves through LDS, normalise, store ------------------
@@ -594,25 +643,25 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // load the ring issued has completed; the barrier ends every read of it.
   wait_loads<0>();
   __builtin_amdgcn_s_barrier();
-  float *xchg = reinterpret_cast<float *>(lds) + rw * (34 * kWave) + lane;
+  float *xchg = reinterpret_cast<float *>(lds) + rw * (G::kXchg * kWave) + lane;
   if (half == 1) {
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a) xchg[(16 * db + a) * kWave] = st.o[db][a];
-    xchg[32 * kWave] = st.m;
-    xchg[33 * kWave] = st.l;
+    xchg[16 * kDB * kWave] = st.m;
+    xchg[(16 * kDB + 1) * kWave] = st.l;
   }
   __syncthreads();
   if (half == 1) return;
   {
-    const float m1 = xchg[32 * kWave];
-    const float l1 = xchg[33 * kWave];
+    const float m1 = xchg[16 * kDB * kWave];
+    const float l1 = xchg[(16 * kDB + 1) * kWave];
     const float m = fmaxf(st.m, m1);
     const float f0 = fast_exp2(st.m - m);
     const float f1 = fast_exp2(m1 - m);
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a)
         st.o[db][a] = st.o[db][a] * f0 + xchg[(16 * db + a) * kWave] * f1;
@@ -624,9 +673,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const float l_tot = st.l + __shfl_xor(st.l, 32);
   const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
   if (my_q < seq) {
-    const size_t row_off = head_off + static_cast<size_t>(my_q) * kHeadDim;
+    const size_t row_off = head_off + static_cast<size_t>(my_q) * D;
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+    for (int db = 0; db < kDB; ++db) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int d = db * 32 + 8 * jj + 4 * g;  // 4 consecutive dims
@@ -647,12 +696,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }
 }
 
-template <bool CAUSAL, bool OUT_F32>
+template <int D, bool CAUSAL, bool OUT_F32>
 void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
                 int seq, int group, float c_scale, bool negate_q, hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
   const unsigned blocks = static_cast<unsigned>(bh) * n_qtiles;
-  hipLaunchKernelGGL((prefill_kernel<CAUSAL, OUT_F32>), dim3(blocks),
+  hipLaunchKernelGGL((prefill_kernel<D, CAUSAL, OUT_F32>), dim3(blocks),
                      dim3(kThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
@@ -662,24 +711,34 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
 
 }  // namespace
 
+template <int D>
+void launch_d(const void *q, const void *k, const void *v, void *o, bool out_f32, int bh,
+              int seq, int group, bool causal, float c_scale, bool negate_q,
+              hipStream_t stream) {
+  if (causal) {
+    if (out_f32)
+      launch_one<D, true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+    else
+      launch_one<D, true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+  } else {
+    if (out_f32)
+      launch_one<D, false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+    else
+      launch_one<D, false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+  }
+}
+
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
                    bool out_f32, int batch, int heads, int kv_heads, int seq,
-                   bool causal, float scale, hipStream_t stream) {
+                   int head_dim, bool causal, float scale, hipStream_t stream) {
   const int bh = batch * heads;
   const int group = heads / kv_heads;
   const float c_scale = fabsf(scale) * kLog2e;
   const bool negate_q = scale < 0.f;
-  if (causal) {
-    if (out_f32)
-      launch_one<true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
-    else
-      launch_one<true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
-  } else {
-    if (out_f32)
-      launch_one<false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
-    else
-      launch_one<false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
-  }
+  if (head_dim == 128)
+    launch_d<128>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, stream);
+  else
+    launch_d<64>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, stream);
   return check_hip(hipGetLastError(), "prefill_kernel launch");
 }
 
@@ -687,9 +746,13 @@ int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n) {
   struct K { const char *name; const void *fn; };
   const K ks[] = {
       {"prefill_kernel<causal=true>",
-       reinterpret_cast<const void *>(prefill_kernel<true, false>)},
+       reinterpret_cast<const void *>(prefill_kernel<64, true, false>)},
       {"prefill_kernel<causal=false>",
-       reinterpret_cast<const void *>(prefill_kernel<false, false>)},
+       reinterpret_cast<const void *>(prefill_kernel<64, false, false>)},
+      {"prefill_kernel<causal=true, head_dim=128>",
+       reinterpret_cast<const void *>(prefill_kernel<128, true, false>)},
+      {"prefill_kernel<causal=false, head_dim=128>",
+       reinterpret_cast<const void *>(prefill_kernel<128, false, false>)},
   };
   for (const K &k : ks) {
     if (*n < cap) {

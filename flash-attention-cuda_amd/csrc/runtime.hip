@@ -141,9 +141,11 @@ int check_groups(int heads, int kv_heads) {
 }
 
 int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_dtype,
-                 int batch, int heads, int kv_heads, int seq, int causal, float scale,
-                 void *stream) {
+                 int batch, int heads, int kv_heads, int seq, int head_dim, int causal,
+                 float scale, void *stream) {
   clear_error();
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128, got %d", head_dim);
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
     return set_error(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
@@ -164,18 +166,21 @@ int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_d
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
   return launch_prefill(q, k, v, o, out_dtype == FA_OUT_F32, batch, heads, kv_heads, seq,
-                        causal != 0, scale, static_cast<hipStream_t>(stream));
+                        head_dim, causal != 0, scale, static_cast<hipStream_t>(stream));
 }
 
 // Resolves split_size 0 to the automatic choice; returns an fa_status.
 // Without grouped queries that is the reference's chooser; with them, the
 // grouped pass's own chunk (it has no reference counterpart).
-int resolve_split(int batch, int heads, int kv_heads, int max_seq, int *split_size) {
+int resolve_split(int batch, int heads, int kv_heads, int max_seq, int head_dim,
+                  int *split_size) {
   if (*split_size < 0)
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "decode split size must be >= 0, got %d", *split_size);
   if (*split_size == 0) {
-    if (kv_heads != heads) {
+    // The matrix-core grouped pass (head_dim 64) has its own chunk policy;
+    // head_dim 128 decodes grouped queries with the per-head VALU kernels.
+    if (kv_heads != heads && head_dim == 64) {
       *split_size =
           decode_group_chunk(batch, decode_units_per_row(heads, kv_heads), max_seq);
       return FA_OK;
@@ -196,29 +201,36 @@ int resolve_split(int batch, int heads, int kv_heads, int max_seq, int *split_si
   return FA_OK;
 }
 
-size_t decode_ws_bytes(int batch, int heads, int max_seq, int split) {
+size_t decode_ws_bytes(int batch, int heads, int max_seq, int head_dim, int split) {
   const size_t n_splits = (static_cast<size_t>(max_seq) + split - 1) / split;
-  return static_cast<size_t>(batch) * heads * n_splits * (FA_HEAD_DIM + 2) *
-         sizeof(float);
+  return static_cast<size_t>(batch) * heads * n_splits * (head_dim + 2) * sizeof(float);
 }
 
-size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq,
+int check_head_dim(int head_dim) {
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128, got %d", head_dim);
+  return FA_OK;
+}
+
+size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq, int head_dim,
                              int split_size) {
   clear_error();
   if (batch <= 0 || heads <= 0 || max_seq <= 0) {
     set_error(FA_ERR_INVALID_ARGUMENT, "batch, heads and max_seq must be > 0");
     return 0;
   }
+  if (check_head_dim(head_dim) != FA_OK) return 0;
   if (check_groups(heads, kv_heads) != FA_OK) return 0;
-  if (resolve_split(batch, heads, kv_heads, max_seq, &split_size) != FA_OK) return 0;
-  return decode_ws_bytes(batch, heads, max_seq, split_size);
+  if (resolve_split(batch, heads, kv_heads, max_seq, head_dim, &split_size) != FA_OK) return 0;
+  return decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
 }
 
 int decode_impl(const void *q, const void *k_cache, const void *v_cache,
                 const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
-                int kv_heads, int max_seq, float scale, int split_size, void *workspace,
-                size_t workspace_bytes, void *stream) {
+                int kv_heads, int max_seq, int head_dim, float scale, int split_size,
+                void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
+  if (check_head_dim(head_dim) != FA_OK) return FA_ERR_INVALID_ARGUMENT;
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       seq_lens == nullptr || o == nullptr)
     return set_error(FA_ERR_INVALID_ARGUMENT,
@@ -242,12 +254,12 @@ int decode_impl(const void *q, const void *k_cache, const void *v_cache,
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
   const bool auto_split = split_size == 0;
-  rc = resolve_split(batch, heads, kv_heads, max_seq, &split_size);
+  rc = resolve_split(batch, heads, kv_heads, max_seq, head_dim, &split_size);
   if (rc != FA_OK) return rc;
   const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
   if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
     return set_error(FA_ERR_INVALID_ARGUMENT, "too many split blocks");
-  const size_t need = decode_ws_bytes(batch, heads, max_seq, split_size);
+  const size_t need = decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(FA_ERR_WORKSPACE,
                      "decode workspace too small: need %zu bytes, got %zu", need,
@@ -255,7 +267,7 @@ int decode_impl(const void *q, const void *k_cache, const void *v_cache,
   if (!aligned16(workspace))
     return set_error(FA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   return launch_decode(q, k_cache, v_cache, seq_lens, o, out_dtype == FA_OUT_F32,
-                       batch, heads, kv_heads, max_seq, scale, split_size, auto_split,
+                       batch, heads, kv_heads, max_seq, head_dim, scale, split_size, auto_split,
                        static_cast<float *>(workspace),
                        static_cast<hipStream_t>(stream));
 }
@@ -267,7 +279,7 @@ int fa_prefill(const void *q, const void *k, const void *v, void *o,
                void *stream) {
   (void)workspace;
   (void)workspace_bytes;
-  return prefill_impl(q, k, v, o, out_dtype, batch, heads, heads, seq, causal, scale,
+  return prefill_impl(q, k, v, o, out_dtype, batch, heads, heads, seq, 64, causal, scale,
                       stream);
 }
 
@@ -276,18 +288,32 @@ int fa_prefill_gqa(const void *q, const void *k, const void *v, void *o, int out
                    void *workspace, size_t workspace_bytes, void *stream) {
   (void)workspace;
   (void)workspace_bytes;
-  return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, causal, scale,
+  return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, 64, causal, scale,
                       stream);
+}
+
+int fa_prefill_hd(const void *q, const void *k, const void *v, void *o, int out_dtype,
+                  int batch, int heads, int kv_heads, int seq, int head_dim, int causal,
+                  float scale, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, head_dim, causal,
+                      scale, stream);
 }
 
 size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
                                  int split_size) {
-  return decode_workspace_impl(batch, heads, heads, max_seq, split_size);
+  return decode_workspace_impl(batch, heads, heads, max_seq, 64, split_size);
 }
 
 size_t fa_decode_gqa_workspace_bytes(int batch, int heads, int kv_heads, int max_seq,
                                      int split_size) {
-  return decode_workspace_impl(batch, heads, kv_heads, max_seq, split_size);
+  return decode_workspace_impl(batch, heads, kv_heads, max_seq, 64, split_size);
+}
+
+size_t fa_decode_hd_workspace_bytes(int batch, int heads, int kv_heads, int max_seq,
+                                    int head_dim, int split_size) {
+  return decode_workspace_impl(batch, heads, kv_heads, max_seq, head_dim, split_size);
 }
 
 int fa_decode(const void *q, const void *k_cache, const void *v_cache,
@@ -295,7 +321,7 @@ int fa_decode(const void *q, const void *k_cache, const void *v_cache,
               int heads, int max_seq, float scale, int split_size,
               void *workspace, size_t workspace_bytes, void *stream) {
   return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, heads,
-                     max_seq, scale, split_size, workspace, workspace_bytes, stream);
+                     max_seq, 64, scale, split_size, workspace, workspace_bytes, stream);
 }
 
 int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
@@ -303,12 +329,23 @@ int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
                   int kv_heads, int max_seq, float scale, int split_size, void *workspace,
                   size_t workspace_bytes, void *stream) {
   return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, kv_heads,
-                     max_seq, scale, split_size, workspace, workspace_bytes, stream);
+                     max_seq, 64, scale, split_size, workspace, workspace_bytes, stream);
 }
 
-int fa_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
-                 int32_t *seq_lens, int batch, int kv_heads, int max_seq, void *stream) {
+int fa_decode_hd(const void *q, const void *k_cache, const void *v_cache,
+                 const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
+                 int kv_heads, int max_seq, int head_dim, float scale, int split_size,
+                 void *workspace, size_t workspace_bytes, void *stream) {
+  return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, kv_heads,
+                     max_seq, head_dim, scale, split_size, workspace, workspace_bytes, stream);
+}
+
+namespace {
+int kv_append_impl(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
+                   int32_t *seq_lens, int batch, int kv_heads, int max_seq, int head_dim,
+                   void *stream) {
   clear_error();
+  if (check_head_dim(head_dim) != FA_OK) return FA_ERR_INVALID_ARGUMENT;
   if (k_cache == nullptr || v_cache == nullptr || k_new == nullptr || v_new == nullptr ||
       seq_lens == nullptr)
     return set_error(FA_ERR_INVALID_ARGUMENT,
@@ -325,7 +362,21 @@ int fa_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_
     return set_error(FA_ERR_INVALID_ARGUMENT, "cache length must be in [1, %d], got %d",
                      kMaxCacheRows, max_seq);
   return launch_kv_append(k_cache, v_cache, k_new, v_new, seq_lens, batch, kv_heads, max_seq,
-                          static_cast<hipStream_t>(stream));
+                          head_dim, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+int fa_kv_append(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
+                 int32_t *seq_lens, int batch, int kv_heads, int max_seq, void *stream) {
+  return kv_append_impl(k_cache, v_cache, k_new, v_new, seq_lens, batch, kv_heads, max_seq,
+                        64, stream);
+}
+
+int fa_kv_append_hd(void *k_cache, void *v_cache, const void *k_new, const void *v_new,
+                    int32_t *seq_lens, int batch, int kv_heads, int max_seq, int head_dim,
+                    void *stream) {
+  return kv_append_impl(k_cache, v_cache, k_new, v_new, seq_lens, batch, kv_heads, max_seq,
+                        head_dim, stream);
 }
 
 int fa_legacy_attention(const float *q, const float *k, const float *v, float *o, int n,

@@ -12,6 +12,10 @@ dividing H; query head h reads K/V head h // (H // H_kv), as
 ``k.repeat_interleave(H // H_kv, dim=1)`` would pair them), without
 materialising the repeated K/V.
 
+Also added: head_dim 128 (``head_dims == (64, 128)``; ``head_dim`` stays 64,
+the reference's value). Every entry point takes the head size from the
+tensors, which must agree on it.
+
 Also added: ``append_kv(k_cache, v_cache, k, v, seq_lens)``, the caller's
 cache write before a decode step (row ``seq_lens[b]``, then ``seq_lens[b] +=
 1``, on the device), so a whole append + decode step can be captured in a
@@ -41,6 +45,7 @@ try:
         decode,
         decode_gqa,
         head_dim,
+        head_dims,
         legacy_fused,
         legacy_naive,
         legacy_tiled,
@@ -63,6 +68,7 @@ __all__ = [
     "decode_gqa",
     "append_kv",
     "head_dim",
+    "head_dims",
     "occupancy_report",
     "choose_decode_split",
     "legacy_naive",

@@ -32,6 +32,11 @@
  *   fa_kv_append             <- no counterpart: the cache write its caller
  *                               (the FlashStack engine, README.md:9-13) does
  *                               before each decode step.
+ *   fa_prefill_hd, fa_decode_hd_workspace_bytes, fa_decode_hd, fa_kv_append_hd
+ *                            <- no counterpart: head_dim 128 is named future
+ *                               work in the reference (README.md:230, :397);
+ *                               with head_dim 64 they are fa_prefill_gqa /
+ *                               fa_decode_gqa / fa_kv_append.
  *   fa_legacy_attention      <- launch_naive_attention / launch_tiled_attention /
  *                               launch_fused_attention,
  *                               src/legacy/{naive,tiled,fused}_attention.cu
@@ -159,6 +164,29 @@ int fa_decode_gqa(const void *q, const void *k_cache, const void *v_cache,
 int fa_kv_append(void *k_cache, void *v_cache, const void *k_new,
                  const void *v_new, int32_t *seq_lens, int batch, int kv_heads,
                  int max_seq, void *stream);
+
+/* head_dim 64 or 128: the entry points above with the head size as an
+ * argument. Tensors are [B, H, S, head_dim] (prefill), [B, H_kv, Lmax,
+ * head_dim] caches and [B, H, 1, head_dim] decode queries / outputs, with
+ * kv_heads dividing heads. Same rules for workspace, split_size, streams and
+ * errors; any other head_dim fails with FA_ERR_INVALID_ARGUMENT. */
+int fa_prefill_hd(const void *q, const void *k, const void *v, void *o,
+                  int out_dtype, int batch, int heads, int kv_heads, int seq,
+                  int head_dim, int causal, float scale, void *workspace,
+                  size_t workspace_bytes, void *stream);
+
+size_t fa_decode_hd_workspace_bytes(int batch, int heads, int kv_heads,
+                                    int max_seq, int head_dim, int split_size);
+
+int fa_decode_hd(const void *q, const void *k_cache, const void *v_cache,
+                 const int32_t *seq_lens, void *o, int out_dtype, int batch,
+                 int heads, int kv_heads, int max_seq, int head_dim, float scale,
+                 int split_size, void *workspace, size_t workspace_bytes,
+                 void *stream);
+
+int fa_kv_append_hd(void *k_cache, void *v_cache, const void *k_new,
+                    const void *v_new, int32_t *seq_lens, int batch,
+                    int kv_heads, int max_seq, int head_dim, void *stream);
 
 /* The reference's v1 single-head kernels: o = softmax(q k^T / sqrt(64)) v
  * for q, k, v, o of shape (n, 64) fp32, row-major, no mask. The three

@@ -36,6 +36,9 @@ What it restates (paths relative to shrvan30/flash-attention-cuda):
 * ``choose_decode_split``: csrc/decode.cu:183-192 (integer closed form).
 * ``attention_flops``: bench/run_bench.py:102-107 (4 B H N^2 d, halved when
   causal). ``decode_bytes``: K and V rows actually read plus q, o, seq_lens.
+* Every function above is written for any head size (the shapes carry it);
+  head_dim 128, the reference's named next step (README.md:397), is pinned
+  like 64 (tests/test_oracle.py).
 * ``make_prefill_inputs`` / ``make_decode_inputs``: the deterministic
   CPU-seeded input recipe used by the tests and the benchmark (torch CPU
   generator seeded with 0, fp32 randn cast to fp16, drawn in the order q, k,
@@ -205,29 +208,31 @@ def decode_bytes(heads: int, seq_lens, max_seq: int, head_dim: int = HEAD_DIM) -
     return kv + qo + 4 * batch
 
 
-def make_prefill_inputs(batch: int, heads: int, seq: int, seed: int = 0):
-    """CPU-seeded fp16 q, k, v of shape [B, H, S, 64] (torch tensors)."""
+def make_prefill_inputs(batch: int, heads: int, seq: int, seed: int = 0,
+                        head_dim: int = HEAD_DIM):
+    """CPU-seeded fp16 q, k, v of shape [B, H, S, head_dim] (torch tensors)."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
-    shape = (batch, heads, seq, HEAD_DIM)
+    shape = (batch, heads, seq, head_dim)
     q = torch.randn(shape, generator=g, dtype=torch.float32).half()
     k = torch.randn(shape, generator=g, dtype=torch.float32).half()
     v = torch.randn(shape, generator=g, dtype=torch.float32).half()
     return q, k, v
 
 
-def make_decode_inputs(batch: int, heads: int, max_seq: int, seed: int = 0, lens=None):
+def make_decode_inputs(batch: int, heads: int, max_seq: int, seed: int = 0, lens=None,
+                       head_dim: int = HEAD_DIM):
     """CPU-seeded decode inputs: lengths (uniform in [1, max_seq] unless given,
-    drawn first), then q [B, H, 1, 64], k_cache, v_cache [B, H, Lmax, 64]."""
+    drawn first), then q [B, H, 1, D], k_cache, v_cache [B, H, Lmax, D]."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
     if lens is None:
         lens = torch.randint(1, max_seq + 1, (batch,), generator=g, dtype=torch.int64)
     lens = torch.as_tensor(lens, dtype=torch.int32)
-    q = torch.randn((batch, heads, 1, HEAD_DIM), generator=g, dtype=torch.float32).half()
-    shape = (batch, heads, max_seq, HEAD_DIM)
+    q = torch.randn((batch, heads, 1, head_dim), generator=g, dtype=torch.float32).half()
+    shape = (batch, heads, max_seq, head_dim)
     k = torch.randn(shape, generator=g, dtype=torch.float32).half()
     v = torch.randn(shape, generator=g, dtype=torch.float32).half()
     return q, k, v, lens

@@ -52,15 +52,19 @@ def test_header_declares_the_expected_entry_points():
             "fa_decode",
             "fa_decode_gqa",
             "fa_decode_gqa_workspace_bytes",
+            "fa_decode_hd",
+            "fa_decode_hd_workspace_bytes",
             "fa_decode_min_blocks",
             "fa_decode_workspace_bytes",
             "fa_head_dim",
             "fa_kv_append",
+            "fa_kv_append_hd",
             "fa_last_error",
             "fa_legacy_attention",
             "fa_occupancy_report",
             "fa_prefill",
             "fa_prefill_gqa",
+            "fa_prefill_hd",
             "fa_prefill_workspace_bytes",
             "fa_version",
         ]
@@ -182,6 +186,21 @@ def test_legacy_attention_argument_checks(lib):
     assert rc == FA_ERR_INVALID_ARGUMENT and b"row count" in lib.fa_last_error()
     # n == 0 computes nothing and launches nothing (no device needed).
     assert lib.fa_legacy_attention(p, p, p, p, 0, 2, None) == FA_OK
+
+
+def test_head_dim_entry_points_reject_other_sizes(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.fa_prefill_hd(p, p, p, p, 0, 1, 2, 2, 8, 96, 1, ctypes.c_float(0.125), None, 0, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"head_dim must be 64 or 128" in lib.fa_last_error()
+    lib.fa_decode_hd_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.fa_decode_hd_workspace_bytes(1, 2, 2, 8, 32, 0) == 0
+    assert b"head_dim must be 64 or 128" in lib.fa_last_error()
+    rc = lib.fa_kv_append_hd(p, p, p, p, p, 1, 1, 8, 256, None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"head_dim must be 64 or 128" in lib.fa_last_error()
+    # The workspace of a forced split grows with head_dim: (D + 2) floats per partial.
+    w64 = lib.fa_decode_hd_workspace_bytes(2, 3, 3, 1000, 64, 256)
+    w128 = lib.fa_decode_hd_workspace_bytes(2, 3, 3, 1000, 128, 256)
+    assert w64 == 2 * 3 * 4 * 66 * 4 and w128 == 2 * 3 * 4 * 130 * 4
 
 
 def test_python_package_exposes_reference_surface():

@@ -68,7 +68,7 @@ def test_append_kv_rejects_bad_shapes():
     kc = torch.zeros(2, 2, 8, 64, dtype=torch.float16, device="cuda")
     k = torch.zeros(2, 2, 1, 64, dtype=torch.float16, device="cuda")
     lens = torch.zeros(2, dtype=torch.int32, device="cuda")
-    with pytest.raises(RuntimeError, match="shape \\[B, H_kv, 1, 64\\]"):
+    with pytest.raises(RuntimeError, match="shape \\[B, H_kv, 1, head_dim\\]"):
         flashattn_cuda.append_kv(kc, kc, k[:, :1].contiguous(), k[:, :1].contiguous(), lens)
     with pytest.raises(RuntimeError, match="seq_lens must be int32"):
         flashattn_cuda.append_kv(kc, kc, k, k, lens.long())

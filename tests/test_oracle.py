@@ -160,6 +160,29 @@ def test_planted_legacy_mistakes_are_caught(kind):
     assert np.abs(oracle.legacy_attention(Q, K, V) - want).max() < 1e-4
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dim_128_prefill_and_decode_match_pins(causal):
+    """The oracle at head_dim 128: torch CPU SDPA in fp32 for prefill, an fp64
+    loop for one decode row, and decode(t) == causal prefill row t."""
+    q, k, v = oracle.make_prefill_inputs(1, 2, 70, seed=4, head_dim=128)
+    assert q.shape == (1, 2, 70, 128)
+    got = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.float(), k.float(), v.float(), is_causal=causal, scale=SCALE).numpy()
+    assert np.abs(got - ref).max() <= 1e-5
+    qd, kd, vd, lens = oracle.make_decode_inputs(2, 1, 9, seed=5, lens=[9, 4], head_dim=128)
+    out = oracle.decode(qd.numpy(), kd.numpy(), vd.numpy(), lens.numpy(), SCALE)
+    Q, K, V = (t.numpy().astype(np.float64) for t in (qd, kd, vd))
+    s = [float(Q[1, 0, 0] @ K[1, 0, j]) * SCALE for j in range(4)]
+    w = np.exp(np.array(s) - max(s))
+    want = (w[:, None] * V[1, 0, :4]).sum(0) / w.sum()
+    assert np.abs(out[1, 0, 0] - want).max() < 2e-6
+    if causal:
+        dec = oracle.decode(q.numpy()[:, :, 69:70], k.numpy(), v.numpy(),
+                            np.array([70]), SCALE)
+        assert np.abs(dec[:, :, 0] - got[:, :, 69]).max() < 1e-6
+
+
 def test_stable_softmax_rows_and_shift_invariance():
     x = np.array([[1.0, 2.0, 3.0], [1000.0, 1001.0, -np.inf]], dtype=np.float32)
     p = oracle.stable_softmax(x)
