@@ -1,7 +1,7 @@
 """Benchmark of the MI355X FlashAttention hot path (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-configs]
-                    [--only all|prefill|decode|copy|gqa|loop]
+                    [--only all|prefill|decode|copy|gqa|loop|d128]
 
 Prints ONE JSON line on stdout (everything else goes to stderr):
 
@@ -68,22 +68,22 @@ def decode_bytes(heads, lens, max_seq, d=64):
     return 2 * heads * d * 2 * int(lens.sum()) + 2 * b * heads * d * 2 + 4 * b
 
 
-def cpu_inputs_prefill(batch, heads, seq, seed=0):
+def cpu_inputs_prefill(batch, heads, seq, seed=0, d=64):
     import torch
 
     g = torch.Generator().manual_seed(seed)
-    shape = (batch, heads, seq, 64)
+    shape = (batch, heads, seq, d)
     return [torch.randn(shape, generator=g, dtype=torch.float32).half() for _ in range(3)]
 
 
-def cpu_inputs_decode(batch, heads, lmax, seed=0):
+def cpu_inputs_decode(batch, heads, lmax, seed=0, d=64):
     import torch
 
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(1, lmax + 1, (batch,), generator=g).to(torch.int32)
-    q = torch.randn((batch, heads, 1, 64), generator=g, dtype=torch.float32).half()
-    k = torch.randn((batch, heads, lmax, 64), generator=g, dtype=torch.float32).half()
-    v = torch.randn((batch, heads, lmax, 64), generator=g, dtype=torch.float32).half()
+    q = torch.randn((batch, heads, 1, d), generator=g, dtype=torch.float32).half()
+    k = torch.randn((batch, heads, lmax, d), generator=g, dtype=torch.float32).half()
+    v = torch.randn((batch, heads, lmax, d), generator=g, dtype=torch.float32).half()
     return q, k, v, lens
 
 
@@ -161,15 +161,15 @@ def timed_steps(fn_list, steps, warmup):
     return wall_ms / steps, start.elapsed_time(end) / steps
 
 
-def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup=0):
+def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup=0, d=64):
     import torch
 
-    q, k, v = (t.cuda() for t in cpu_inputs_prefill(batch, heads, seq))
+    q, k, v = (t.cuda() for t in cpu_inputs_prefill(batch, heads, seq, d=d))
     n = copies_for(3 * q.numel() * 2) if protocol == "ref" else 1
     sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
     fns = [lambda s=s: fa.prefill(s[0], s[1], s[2], causal, SCALE) for s in sets]
     torch.cuda.synchronize()
-    flops = attention_flops(batch, heads, seq, causal)
+    flops = attention_flops(batch, heads, seq, causal, d)
     if protocol == "ref":
         ms = ref_timeit(fns)
         return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "copies": n}
@@ -177,10 +177,10 @@ def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup
     return {"ms_per_step": step_ms, "kernel_ms": kern_ms, "flops": flops}
 
 
-def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, warmup=0):
+def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, warmup=0, d=64):
     import torch
 
-    q, k, v, rl = cpu_inputs_decode(batch, heads, lmax)
+    q, k, v, rl = cpu_inputs_decode(batch, heads, lmax, d=d)
     if lens is not None:
         rl = torch.tensor(lens, dtype=torch.int32)
     q, k, v, rl = q.cuda(), k.cuda(), v.cuda(), rl.cuda()
@@ -188,7 +188,7 @@ def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, war
     sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
     fns = [lambda s=s: fa.decode(s[0], s[1], s[2], rl, SCALE) for s in sets]
     torch.cuda.synchronize()
-    nbytes = decode_bytes(heads, rl.cpu(), lmax)
+    nbytes = decode_bytes(heads, rl.cpu(), lmax, d)
     if protocol == "ref":
         ms = ref_timeit(fns)
         return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "copies": n}
@@ -238,6 +238,28 @@ def bench_gqa(fa):
                  HBM_PEAK_GBS, "copies": n, "ms_repeat_then_decode": ms_rep})
     log(f"  {rows[-1]['config']}: {ms * 1e3:.1f} us ({rows[-1]['gbs']:.1f} GB/s); "
         f"repeat + decode {ms_rep * 1e3:.1f} us")
+    return rows
+
+
+def bench_head_dim_128(fa):
+    """head_dim 128 (the reference's named next step, README.md:397) at the
+    config 3, config 2 (full) and config 5 shapes, reference timing protocol.
+    FLOPs 4 B H S^2 128 (halved when causal); decode bytes count the K/V rows
+    read (256 B each per head), q, o and seq_lens."""
+    rows = []
+    for name, b, h, s, c in [("C3-shape causal B1 H14 S4096 D128", 1, 14, 4096, True),
+                             ("C2-shape full B4 H12 S1024 D128", 4, 12, 1024, False)]:
+        r = bench_prefill(fa, b, h, s, c, d=128)
+        rows.append({"config": name, "ms": r["ms"], "tflops": r["tflops"],
+                     "frac_mfma": r["tflops"] / MFMA_FP16_PEAK_TFLOPS})
+        log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['tflops']:.1f} TFLOP/s")
+    for name, b, h, lmax, lens in [("C4-shape decode B1 H12 L4096 D128", 1, 12, 4096, [4096]),
+                                   ("C5-shape ragged decode B32 H14 Lmax4096 D128", 32, 14,
+                                    4096, None)]:
+        r = bench_decode(fa, b, h, lmax, lens=lens, d=128)
+        rows.append({"config": name, "ms": r["ms"], "gbs": r["gbs"],
+                     "frac_hbm": r["gbs"] / HBM_PEAK_GBS, "copies": r["copies"]})
+        log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['gbs']:.1f} GB/s")
     return rows
 
 
@@ -410,10 +432,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config sweep")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy", "gqa", "loop"],
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "copy", "gqa", "loop", "d128"],
                     default="all",
                     help="copy: only the 1 GiB copy that calibrates the HBM byte counters; "
-                         "gqa: only the grouped-query lines; loop: only the decode loop")
+                         "gqa: only the grouped-query lines; loop: only the decode loop; "
+                         "d128: only the head_dim 128 lines")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -445,6 +468,13 @@ def main():
         print(json.dumps({"metric": "decode loop tokens/s (append_kv + decode per token)",
                           "value": rows[-1]["tok_s_graph"], "unit": "tokens/s",
                           "decode_loop": rows}), flush=True)
+        return
+
+    if args.only == "d128":
+        rows = bench_head_dim_128(fa)
+        print(json.dumps({"metric": "head_dim 128 prefill TFLOP/s and decode KV GB/s",
+                          "value": rows[0]["tflops"], "unit": "TFLOP/s",
+                          "head_dim_128": rows}), flush=True)
         return
 
     if args.only == "gqa":
@@ -539,6 +569,8 @@ def main():
         result["gqa"] = bench_gqa(fa)
         log("decode loop: append_kv + decode per token ...")
         result["decode_loop"] = bench_decode_loop(fa)
+        log("head_dim 128 (no reference counterpart) ...")
+        result["head_dim_128"] = bench_head_dim_128(fa)
 
     if not args.no_cpu:
         log("CPU baseline (oracle, bounded sample) ...")
