@@ -43,7 +43,8 @@ BENCH=0
 if [[ $# -gt 0 ]]; then
   WORKLOADS=("$@")
 else
-  WORKLOADS=(copy_1g prefill_c3 prefill_c2_causal prefill_c2_full decode_c4 decode_c5 decode_gqa_c5)
+  WORKLOADS=(copy_1g prefill_c3 prefill_c2_causal prefill_c2_full decode_c4 decode_c5 decode_gqa_c5
+             prefill_c3_d128 decode_c5_d128)
   BENCH=1
 fi
 mkdir -p "${OUT}"

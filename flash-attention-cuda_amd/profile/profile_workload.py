@@ -32,16 +32,21 @@ MALL_BYTES = 256 << 20
 
 # name -> (description, main kernel (short name prefix), unit, work per call)
 WORKLOADS = {
-    "prefill_c3": ("config 3: causal prefill B=1 H=14 S=4096", "prefill_kernel<true",
+    "prefill_c3": ("config 3: causal prefill B=1 H=14 S=4096", "prefill_kernel<64, true",
                    "flop", 4.0 * 14 * 4096 * 4096 * 64 / 2),
-    "prefill_c2_causal": ("config 2: causal prefill B=4 H=12 S=1024", "prefill_kernel<true",
+    "prefill_c2_causal": ("config 2: causal prefill B=4 H=12 S=1024", "prefill_kernel<64, true",
                           "flop", 4.0 * 4 * 12 * 1024 * 1024 * 64 / 2),
-    "prefill_c2_full": ("config 2: full prefill B=4 H=12 S=1024", "prefill_kernel<false",
+    "prefill_c2_full": ("config 2: full prefill B=4 H=12 S=1024", "prefill_kernel<64, false",
                         "flop", 4.0 * 4 * 12 * 1024 * 1024 * 64),
+    "prefill_c3_d128": ("config 3 shape at head_dim 128: causal prefill B=1 H=14 S=4096 D=128",
+                        "prefill_kernel<128, true", "flop", 4.0 * 14 * 4096 * 4096 * 128 / 2),
     "decode_c4": ("config 4: decode B=1 H=12 L=4096 (split-K + merge)", "decode_split_kernel",
                   "byte", 2 * 12 * 64 * 2 * 4096 + 2 * 12 * 64 * 2 + 4),
     "decode_c5": ("config 5: ragged decode B=32 H=14 Lmax=4096, lens U[1,4096] seed 0",
                   "decode_bh_kernel", "byte", 2 * 14 * 64 * 2 * 73374 + 2 * 32 * 14 * 64 * 2 + 128),
+    "decode_c5_d128": ("config 5 shape at head_dim 128: ragged decode B=32 H=14 Lmax=4096 D=128",
+                       "decode_bh_kernel<128", "byte",
+                       2 * 14 * 128 * 2 * 73374 + 2 * 32 * 14 * 128 * 2 + 128),
     "decode_gqa_c5": ("config 5 batch with 2 K/V heads (group 7): grouped decode",
                       "decode_group_kernel", "byte", 2 * 2 * 64 * 2 * 73374 + 2 * 32 * 14 * 64 * 2 + 128),
     "copy_1g": ("1 GiB device copy (byte-counter calibration)", "copyBuffer", "byte",
@@ -72,27 +77,27 @@ def _run(fns):
     torch.cuda.synchronize()
 
 
-def _prefill(batch, heads, seq, causal):
+def _prefill(batch, heads, seq, causal, d=64):
     import torch
 
     import flashattn_cuda as fa
 
     g = torch.Generator().manual_seed(0)
-    shape = (batch, heads, seq, 64)
+    shape = (batch, heads, seq, d)
     q, k, v = (torch.randn(shape, generator=g).half().cuda() for _ in range(3))
     _run([lambda: fa.prefill(q, k, v, causal, SCALE)])
 
 
-def _decode_inputs(batch, heads, lmax, lens=None):
+def _decode_inputs(batch, heads, lmax, lens=None, d=64):
     import torch
 
     g = torch.Generator().manual_seed(0)
     rl = torch.randint(1, lmax + 1, (batch,), generator=g).to(torch.int32)
     if lens is not None:
         rl = torch.tensor(lens, dtype=torch.int32)
-    q = torch.randn((batch, heads, 1, 64), generator=g).half()
-    k = torch.randn((batch, heads, lmax, 64), generator=g).half()
-    v = torch.randn((batch, heads, lmax, 64), generator=g).half()
+    q = torch.randn((batch, heads, 1, d), generator=g).half()
+    k = torch.randn((batch, heads, lmax, d), generator=g).half()
+    v = torch.randn((batch, heads, lmax, d), generator=g).half()
     return q, k, v, rl
 
 
@@ -100,10 +105,10 @@ def _copies(nbytes):
     return max(1, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
 
 
-def _decode(batch, heads, lmax, lens=None, kv_every=1):
+def _decode(batch, heads, lmax, lens=None, kv_every=1, d=64):
     import flashattn_cuda as fa
 
-    q, k, v, rl = _decode_inputs(batch, heads, lmax, lens)
+    q, k, v, rl = _decode_inputs(batch, heads, lmax, lens, d)
     call = fa.decode
     if kv_every > 1:  # grouped: keep K/V heads 0, G, 2G, ...
         k, v = k[:, ::kv_every].contiguous(), v[:, ::kv_every].contiguous()
@@ -126,9 +131,11 @@ RUNNERS = {
     "prefill_c3": lambda: _prefill(1, 14, 4096, True),
     "prefill_c2_causal": lambda: _prefill(4, 12, 1024, True),
     "prefill_c2_full": lambda: _prefill(4, 12, 1024, False),
+    "prefill_c3_d128": lambda: _prefill(1, 14, 4096, True, d=128),
     "decode_c4": lambda: _decode(1, 12, 4096, lens=[4096]),
     "decode_c5": lambda: _decode(32, 14, 4096),
     "decode_gqa_c5": lambda: _decode(32, 14, 4096, kv_every=7),
+    "decode_c5_d128": lambda: _decode(32, 14, 4096, d=128),
     "copy_1g": _copy,
 }
 

@@ -36,6 +36,10 @@ def test_mangled_names_are_demangled_and_instantiations_stay_apart():
     causal = rx.short_kernel_name("_ZN2fa12_GLOBAL__N_114prefill_kernelILb1ELb0EEEvPKDF16_S3_S3_Pviiifb")
     full = rx.short_kernel_name("_ZN2fa12_GLOBAL__N_114prefill_kernelILb0ELb0EEEvPKDF16_S3_S3_Pviiifb")
     assert causal == "prefill_kernel<true, false>" and full == "prefill_kernel<false, false>"
+    # The head size is the first template argument of the current kernels.
+    d128 = rx.short_kernel_name(
+        "_ZN2fa12_GLOBAL__N_114prefill_kernelILi128ELb1ELb0EEEvPKDF16_S3_S3_Pviiifb")
+    assert d128 == "prefill_kernel<128, true, false>"
     assert rx.short_kernel_name(
         "_ZN2fa12_GLOBAL__N_119decode_group_kernelEPKDF16_S2_S2_PKiPfS5_iiiiiiiif") == \
         "decode_group_kernel"
@@ -46,7 +50,7 @@ def test_mangled_names_are_demangled_and_instantiations_stay_apart():
 
 
 STATS = '''"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"
-"void fa::(anonymous namespace)::prefill_kernel<true, false>(_Float16 const*)",25,1250000,50000.0,90.0,48000,52000,100.0
+"void fa::(anonymous namespace)::prefill_kernel<64, true, false>(_Float16 const*)",25,1250000,50000.0,90.0,48000,52000,100.0
 "__amd_rocclr_copyBuffer",2,20000,10000.0,10.0,9000,11000,5.0
 '''
 
@@ -67,7 +71,7 @@ def _write(path, text):
         handle.write(text)
 
 
-PK = "void fa::(anonymous namespace)::prefill_kernel<true, false>(_Float16 const*)"
+PK = "void fa::(anonymous namespace)::prefill_kernel<64, true, false>(_Float16 const*)"
 
 
 def _tree(root):
@@ -94,10 +98,10 @@ def test_parsers(tmp_path):
     root = str(tmp_path)
     _tree(root)
     stats = rx.read_kernel_stats(f"{root}/prefill_c3/trace/run_kernel_stats.csv")
-    assert stats["prefill_kernel<true, false>"]["calls"] == 25
-    assert stats["prefill_kernel<true, false>"]["avg_us"] == 50.0
+    assert stats["prefill_kernel<64, true, false>"]["calls"] == 25
+    assert stats["prefill_kernel<64, true, false>"]["avg_us"] == 50.0
     counters = rx.read_counters(f"{root}/prefill_c3/fetch/run_counter_collection.csv")
-    assert counters["prefill_kernel<true, false>"]["FETCH_SIZE"] == 15000.0  # mean of dispatches
+    assert counters["prefill_kernel<64, true, false>"]["FETCH_SIZE"] == 15000.0  # mean of dispatches
     assert rx.calibration(root) == (2048.0, 1024.0)
 
 
@@ -106,16 +110,16 @@ def test_analyse_and_render(tmp_path):
     _tree(root)
     report = rx.analyse(root)
     w = report["workloads"]["prefill_c3"]
-    k = w["kernels"]["prefill_kernel<true, false>"]
+    k = w["kernels"]["prefill_kernel<64, true, false>"]
     assert k["read_bytes"] == 15000.0 * 2048 and k["write_bytes"] == 7168 * 1024
     assert k["mfma_util_pct"] == 31.0 and k["occupancy_pct"] == 25.0
     main = w["main"]
-    assert main["kernel"] == "prefill_kernel<true, false>"
+    assert main["kernel"] == "prefill_kernel<64, true, false>"
     # config 3: 30,064,771,072 FLOP in 50 us
     assert abs(main["rate"] - 30064771072.0 / 50e-6) < 1.0
     assert abs(main["frac"] - main["rate"] / 2516.6e12) < 1e-12
     text = rx.render(report, "bash profile_rocprof.sh")
-    assert "prefill_kernel<true, false>" in text and "bash profile_rocprof.sh" in text
+    assert "prefill_kernel<64, true, false>" in text and "bash profile_rocprof.sh" in text
     assert f"{100 * main['frac']:.1f} %" in text
     assert "31.0 %" in text and "30.72 MB" in text  # 15000 KiB x 2048 B/KiB
     # Workloads without traces are left out, not rendered empty.
@@ -135,7 +139,7 @@ def test_bench_runs_pair_trace_and_events(tmp_path):
            'timing ...\n{"value": 600.0, "roofline": {"kernel": "prefill_kernel<causal=true>", '
            '"kernel_ms": 0.0495, "achieved": 607.4, "unit": "TFLOP/s"}}\n')
     runs = rx.bench_runs(root)
-    assert runs["prefill"]["kernel"] == "prefill_kernel<true, false>"
+    assert runs["prefill"]["kernel"] == "prefill_kernel<64, true, false>"
     assert runs["prefill"]["trace_avg_us"] == 50.0
     assert abs(runs["prefill"]["bench_event_us"] - 49.5) < 1e-9
     assert "bench_decode" not in runs and "decode" not in runs
