@@ -8,14 +8,14 @@
 // cores with fp32 accumulation.
 //
 // What bounds this kernel on gfx950 (measured):
-//   * One v_mfma_f32_32x32x16_f16 occupies its SIMD for ~17 ns. VALU work of
-//     OTHER waves on the same SIMD does not run meanwhile; VALU work of the
-//     SAME wave placed between its MFMAs partly does (a few VALU ops, or
-//     ~4 v_exp_f32, per MFMA hide almost completely). The softmax is about as
-//     much VALU time as the two products are MFMA time, so each wave runs a
+//   * One v_mfma_f32_32x32x16_f16 occupies the matrix core of its SIMD for
+//     ~16 ns. One wave issues VALU at half the SIMD's rate, two waves at the
+//     full rate; VALU work of the other wave mostly runs while an MFMA does
+//     (v_exp_f32 partly, v_dot2c_f32_f16 not at all). The softmax is more
+//     VALU time than the two products are MFMA time, so each wave runs a
 //     software pipeline: the MFMAs of its neighbouring tiles interleave with
-//     the softmax of the current one. The second wave on each SIMD covers the
-//     latencies (barrier, LDS reads, loads) of the first.
+//     the softmax of the current one, and the second wave on each SIMD fills
+//     the VALU and covers the latencies (barrier, LDS reads, loads).
 //   * LDS serves ~one 64-lane read instruction per 3 ns per CU.
 //
 // Work decomposition
