@@ -260,6 +260,29 @@ def bench_head_dim_128(fa):
         rows.append({"config": name, "ms": r["ms"], "gbs": r["gbs"],
                      "frac_hbm": r["gbs"] / HBM_PEAK_GBS, "copies": r["copies"]})
         log(f"  {name}: {r['ms'] * 1e3:.1f} us, {r['gbs']:.1f} GB/s")
+    # Grouped queries at head_dim 128 (2 K/V heads for 14 query heads): the
+    # matrix-core grouped pass against repeat-then-decode.
+    import torch
+
+    kv_heads, heads, group = 2, 14, 7
+    qd, kd, vd, rl = cpu_inputs_decode(32, heads, 4096, d=128)
+    kd, vd = kd[:, ::group].contiguous(), vd[:, ::group].contiguous()
+    qd, rl = qd.cuda(), rl.cuda()
+    n = copies_for(2 * kd.numel() * 2)
+    sets = [(kd.cuda(), vd.cuda())]
+    sets += [tuple(t.clone() for t in sets[0]) for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    nbytes = decode_bytes(kv_heads, rl.cpu(), 4096, 128) + 2 * 32 * (heads - kv_heads) * 128 * 2
+    ms = ref_timeit([lambda s=s: fa.decode_gqa(qd, s[0], s[1], rl, SCALE) for s in sets])
+    ms_rep = ref_timeit([lambda s=s: fa.decode(qd, s[0].repeat_interleave(group, 1),
+                                               s[1].repeat_interleave(group, 1), rl, SCALE)
+                         for s in sets])
+    rows.append({"config": "C5-shape GQA ragged decode B32 H14 Hkv2 Lmax4096 D128", "ms": ms,
+                 "gbs": nbytes / (ms * 1e-3) / 1e9,
+                 "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "copies": n,
+                 "ms_repeat_then_decode": ms_rep})
+    log(f"  {rows[-1]['config']}: {ms * 1e3:.1f} us ({rows[-1]['gbs']:.1f} GB/s); "
+        f"repeat + decode {ms_rep * 1e3:.1f} us")
     return rows
 
 

@@ -204,13 +204,12 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
 // Pass 1 (decode.cu:50-138): one wave folds cache rows
 // [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
 // partial (m, l, acc[D]). Unit u = chunk_i * (B * H) + (b * H + h) is
-// handled by wave u % 4 of block u / 4. With grouped queries (group > 1,
-// head_dim 128 only) query head bh reads cache head bh / group.
+// handled by wave u % 4 of block u / 4.
 template <int D>
 __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
-    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads, int group,
+    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads,
     int max_seq, int n_splits, int n_units, int chunk, float qscale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int unit = static_cast<int>(blockIdx.x) * kSplitWaves +
@@ -235,7 +234,7 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   if (begin >= len) return;
   const int end = min(len, begin + chunk);
 
-  const size_t head_off = static_cast<size_t>(bh / group) * max_seq * D;
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
   const _Float16 *kp = k_cache + head_off;
   const _Float16 *vp = v_cache + head_off;
 
@@ -393,11 +392,23 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(
 // read once for its whole group at HBM speed, where the VALU path above pays
 // the dot products and the P V update once per query.
 constexpr int kGroupTile = 32;                           // cache rows per tile
-constexpr int kGroupStages = 4;                          // ring depth per wave (2..4)
-constexpr int kGroupAhead = kGroupStages - 1;            // tiles in flight
-constexpr int kGroupTileHalves = kGroupTile * kHeadDim;  // 4 KiB
-constexpr int kGroupLoads = 2 * kGroupTile / 8;          // K + V loads per lane per tile
 constexpr int kGroupCols = 32;                           // queries per wave
+
+// Ring geometry of the grouped pass for head_dim D. A tile is 32 rows of
+// 2 D bytes (4 KiB at D = 64, 8 KiB at D = 128); the ring depth keeps the
+// per-wave LDS at 32 KiB (5 waves per CU) for D = 64 and 48 KiB (3 waves per
+// CU) for D = 128.
+template <int D>
+struct GroupGeo {
+  static constexpr int kStages = D == 64 ? 4 : 3;        // ring depth per wave (2..4)
+  static constexpr int kAhead = kStages - 1;             // tiles in flight
+  static constexpr int kTileHalves = kGroupTile * D;
+  static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
+  static constexpr int kRowsPerLoad = kWave / kChunks;   // 8 or 4
+  static constexpr int kRowBlocks = kGroupTile / kRowsPerLoad;  // 4 or 8
+  static constexpr int kLoads = 2 * kRowBlocks;          // K + V loads per lane per tile
+  static constexpr int kWavesPerCu = (160 * 1024) / (2 * kStages * kTileHalves * 2);
+};
 
 constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
 
@@ -406,10 +417,10 @@ constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every t
 // lane's share of the row sum. MASK: rows >= lim of this lane's half are past
 // the chunk end. SPLIT: P as fp16 hi + lo (two PV products) instead of one
 // fp16 rounding; l sums the same fp16 values the products consume.
-template <bool MASK, bool SPLIT>
-__device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&vf)[2][2],
+template <int D, bool MASK, bool SPLIT>
+__device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&vf)[2][D / 32],
                                                  int lim, float c, float &m, float &l,
-                                                 floatx16 (&o)[2]) {
+                                                 floatx16 (&o)[D / 32]) {
   float mx = -INFINITY;
 #pragma unroll
   for (int a = 0; a < 16; ++a) {
@@ -450,24 +461,32 @@ __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&v
   // alpha is exactly 1 wherever the max did not rise (wave-uniform branch).
   if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a) o[db][a] *= alpha;
   }
 #pragma unroll
   for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+    for (int db = 0; db < D / 32; ++db) {
       o[db] = mfma(vf[hs][db], p_hi[hs], o[db]);
       if (SPLIT) o[db] = mfma(vf[hs][db], p_lo[hs], o[db]);
     }
 }
 
+template <int D>
 __global__ __launch_bounds__(kWave) void decode_group_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
     float *__restrict__ part_acc, float *__restrict__ part_ml, int heads, int kv_heads,
     int group, int nq, int max_seq, int n_splits, int n_units, int chunk, float qscale) {
+  using G = GroupGeo<D>;
+  constexpr int kGroupStages = G::kStages;
+  constexpr int kGroupAhead = G::kAhead;
+  constexpr int kGroupTileHalves = G::kTileHalves;
+  constexpr int kGroupLoads = G::kLoads;
+  constexpr int kDS = D / 16;  // k-steps of S^T = K Q^T
+  constexpr int kDB = D / 32;  // d-blocks of O^T
   __shared__ __attribute__((aligned(1024))) _Float16 lds[2 * kGroupStages * kGroupTileHalves];
   const int unit = static_cast<int>(blockIdx.x);
   if (unit >= n_units) return;
@@ -484,51 +503,52 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
   const int end = min(len, begin + chunk);
   const int n_tiles = (end - begin + kGroupTile - 1) / kGroupTile;
 
-  const size_t kv_off = (static_cast<size_t>(qu.b) * kv_heads + qu.kv) * max_seq * kHeadDim;
+  const size_t kv_off = (static_cast<size_t>(qu.b) * kv_heads + qu.kv) * max_seq * D;
   const _Float16 *const kp = k_cache + kv_off;
   const _Float16 *const vp = v_cache + kv_off;
   _Float16 *const kring = lds;
   _Float16 *const vring = lds + kGroupStages * kGroupTileHalves;
 
-  // Loads of tile t: lane = 8 * (row in an 8-row block) + 16-byte chunk; four
-  // row blocks each of K and V. Rows past the chunk end are clamped to its
-  // last row (they are masked out of the softmax).
-  const int r8 = lane >> 3;
-  const int c16 = lane & 7;
-  int src_k[4], src_v[4];
+  // Loads of tile t: lane = (D / 8) * (row in a row block) + 16-byte chunk;
+  // 32 / (512 / D) row blocks each of K and V. Rows past the chunk end are
+  // clamped to its last row (they are masked out of the softmax).
+  const int rr = lane / G::kChunks;
+  const int c16 = lane % G::kChunks;
+  int src_k[G::kRowBlocks], src_v[G::kRowBlocks];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    const int r = rb * 8 + r8;  // row inside the tile (tile rows start at a multiple of 32)
-    src_k[rb] = (c16 ^ k_swz(r)) << 3;
-    src_v[rb] = (c16 ^ v_swz(r)) << 3;
+  for (int rb = 0; rb < G::kRowBlocks; ++rb) {
+    const int r = rb * G::kRowsPerLoad + rr;  // row inside the tile (tiles start at a multiple of 32)
+    src_k[rb] = (c16 ^ k_swz_d<D>(r)) << 3;
+    src_v[rb] = (c16 ^ v_swz_d<D>(r)) << 3;
   }
   auto issue = [&](int t) {
     const int row0 = begin + t * kGroupTile;
     _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
     _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const size_t row = static_cast<size_t>(min(row0 + rb * 8 + r8, end - 1)) * kHeadDim;
-      global_to_lds16(kp + row + src_k[rb], ks + rb * 8 * kHeadDim);
-      global_to_lds16(vp + row + src_v[rb], vs + rb * 8 * kHeadDim);
+    for (int rb = 0; rb < G::kRowBlocks; ++rb) {
+      const size_t row =
+          static_cast<size_t>(min(row0 + rb * G::kRowsPerLoad + rr, end - 1)) * D;
+      global_to_lds16(kp + row + src_k[rb], ks + rb * G::kRowsPerLoad * D);
+      global_to_lds16(vp + row + src_v[rb], vs + rb * G::kRowsPerLoad * D);
     }
   };
   // Q^T fragments: column `col` is query head h0 + col of the unit (zeros
-  // past nq), head dims [32 g + 8 s, +8) for k-step s. They are waited for
+  // past nq), head dims [(D / 2) g + 8 s, +8) for k-step s. They are waited for
   // here, before the ring's first loads: a Q load still pending inside the
   // loop would make the compiler wait for every load (ring included) there.
-  half8 qf[4];
+  half8 qf[kDS];
   const size_t bh0 = static_cast<size_t>(qu.b) * heads + qu.h0;
   const int qcol = min(col, nq - 1);  // columns past nq load a valid row, then zero it
 #pragma unroll
-  for (int st = 0; st < 4; ++st)
-    qf[st] = *reinterpret_cast<const half8 *>(q + (bh0 + qcol) * kHeadDim + 32 * g + 8 * st);
+  for (int st = 0; st < kDS; ++st)
+    qf[st] = *reinterpret_cast<const half8 *>(q + (bh0 + qcol) * D + (D / 2) * g + 8 * st);
   // A negative scale is folded into Q (an exact fp16 negation), so the
   // softmax works with c = |scale| log2(e) > 0 and takes its max on the raw
   // scores.
   const float c_scale = fabsf(qscale);
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
+  for (int st = 0; st < kDS; ++st) {
     if (col >= nq) qf[st] = half8{};
     if (qscale < 0.f) qf[st] = -qf[st];
     asm volatile("" ::"v"(qf[st]));
@@ -538,11 +558,11 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
   for (int t = 0; t < kGroupAhead; ++t)
     if (t < n_tiles) issue(t);
 
-  const FragOffsets fo = frag_offsets(lane);
+  const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
   float m = kNegBig, l = 0.f;
-  floatx16 o[2];
+  floatx16 o[kDB];
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+  for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int a = 0; a < 16; ++a) o[db][a] = 0.f;
 
@@ -564,19 +584,19 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
         wait_loads<0>();
       const _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
       const _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
-      half8 kf[4];
+      half8 kf[kDS];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) kf[st] = *reinterpret_cast<const half8 *>(ks + fo.k[st]);
-      half8 vf[2][2];  // [16-row step][d-block]
+      for (int st = 0; st < kDS; ++st) kf[st] = *reinterpret_cast<const half8 *>(ks + fo.k[st]);
+      half8 vf[2][kDB];  // [16-row step][d-block]
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
+      for (int db = 0; db < kDB; ++db) {
         lds_half *pv = opaque_lds(vs + fo.v[db]);
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
           for (int part = 0; part < 2; ++part) {
             const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v *)(pv + (16 * hs + 8 * part) * kHeadDim));
+                (__attribute__((address_space(3))) short4v *)(pv + (16 * hs + 8 * part) * D));
             const half4 v4 = __builtin_bit_cast(half4, r);
 #pragma unroll
             for (int e = 0; e < 4; ++e) vf[hs][db][4 * part + e] = v4[e];
@@ -590,13 +610,13 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
 #pragma unroll
       for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) sacc = mfma(kf[st], qf[st], sacc);
+      for (int st = 0; st < kDS; ++st) sacc = mfma(kf[st], qf[st], sacc);
       if (partial_tail && t == n_tiles - 1) {
         // Element a: row 8 (a / 4) + 4 g + a % 4 of the tile.
         const int lim = end - (begin + t * kGroupTile) - 4 * g;
-        group_softmax_pv<true, SPLIT>(sacc, vf, lim, c_scale, m, l, o);
+        group_softmax_pv<D, true, SPLIT>(sacc, vf, lim, c_scale, m, l, o);
       } else {
-        group_softmax_pv<false, SPLIT>(sacc, vf, 0, c_scale, m, l, o);
+        group_softmax_pv<D, false, SPLIT>(sacc, vf, 0, c_scale, m, l, o);
       }
     }
   };
@@ -606,13 +626,13 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     run(std::false_type{});
 
   // Lanes l and l ^ 32 hold the two row halves of column col: m is shared,
-  // l adds up; each lane writes its 32 of the 64 head dims.
+  // l adds up; each lane writes its half of the D head dims.
   l += __shfl_xor(l, 32);
   if (col < nq) {
     const size_t slot = (bh0 + col) * n_splits + split;
-    float *const dst = part_acc + slot * kHeadDim;
+    float *const dst = part_acc + slot * D;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb)
         *reinterpret_cast<float4 *>(dst + db * 32 + 8 * rb + 4 * g) =
@@ -647,7 +667,7 @@ template <int D, bool OUT_F32>
 __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
     const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
-    void *__restrict__ o, int batch, int heads, int group, int max_seq, int chunk,
+    void *__restrict__ o, int batch, int heads, int max_seq, int chunk,
     int target_waves, float qscale) {
   __shared__ int s_len[kRankMax];
   __shared__ int s_order[kRankMax];
@@ -700,7 +720,7 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
 
   const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
   const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
-  const size_t head_off = static_cast<size_t>(bh / group) * max_seq * D;
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
   const _Float16 *kp = k_cache + head_off;
   const _Float16 *vp = v_cache + head_off;
 
@@ -821,9 +841,7 @@ int group_queries(int group) {
   return 1;
 }
 
-// Waves of decode_group_kernel the automatic chunk aims at: the 5 per CU its
-// LDS ring lets run at once.
-constexpr int kGroupWavesPerCu = 5;
+
 
 }  // namespace
 
@@ -833,11 +851,14 @@ int decode_units_per_row(int heads, int kv_heads) {
   return kv_heads * (group / group_queries(group));
 }
 
-int decode_group_chunk(int batch, int units_per_row, int max_seq) {
+int decode_group_chunk(int batch, int units_per_row, int max_seq, int head_dim) {
   int dev = 0;
   int cu = 0;
   if (hipGetDevice(&dev) == hipSuccess) cu = device_cu_count(dev);
-  const long long waves = static_cast<long long>(kGroupWavesPerCu) * (cu > 0 ? cu : 256);
+  // The waves of decode_group_kernel its LDS ring lets run at once per CU.
+  const int per_cu =
+      head_dim == 128 ? GroupGeo<128>::kWavesPerCu : GroupGeo<64>::kWavesPerCu;
+  const long long waves = static_cast<long long>(per_cu) * (cu > 0 ? cu : 256);
   const long long work = static_cast<long long>(max_seq) * batch * units_per_row;
   long long rows = (work + waves - 1) / waves;
   rows = ((rows + kGroupTile - 1) / kGroupTile) * kGroupTile;
@@ -848,13 +869,13 @@ int decode_group_chunk(int batch, int units_per_row, int max_seq) {
 
 namespace {
 
-// The VALU kernels for head_dim D: the whole-sequence kernel when B * H fills
-// the chip (or the cache is short), else split-K and the merge. group > 1
-// (head_dim 128 only) makes query head bh read K/V head bh / group.
+// The VALU kernels for head_dim D (no grouped queries): the whole-sequence
+// kernel when B * H fills the chip (or the cache is short), else split-K and
+// the merge.
 template <int D>
 int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
                        const int32_t *seq_lens, void *o, bool out_f32, int batch, int heads,
-                       int group, int max_seq, float scale, int split_size, bool auto_split,
+                       int max_seq, float scale, int split_size, bool auto_split,
                        float *workspace, hipStream_t stream) {
   const int n_splits = (max_seq + split_size - 1) / split_size;
   const size_t bh = static_cast<size_t>(batch) * heads;
@@ -870,14 +891,14 @@ int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
                          dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
                          static_cast<const _Float16 *>(k_cache),
                          static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
-                         heads, group, max_seq, auto_split ? 0 : split_size,
+                         heads, max_seq, auto_split ? 0 : split_size,
                          target_waves, scale * kLog2e);
     else
       hipLaunchKernelGGL((decode_bh_kernel<D, false>), dim3(static_cast<unsigned>(bh)),
                          dim3(kBhThreads), 0, stream, static_cast<const _Float16 *>(q),
                          static_cast<const _Float16 *>(k_cache),
                          static_cast<const _Float16 *>(v_cache), seq_lens, o, batch,
-                         heads, group, max_seq, auto_split ? 0 : split_size,
+                         heads, max_seq, auto_split ? 0 : split_size,
                          target_waves, scale * kLog2e);
     return check_hip(hipGetLastError(), "decode_bh_kernel launch");
   }
@@ -892,7 +913,7 @@ int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k_cache),
                      static_cast<const _Float16 *>(v_cache), seq_lens,
-                     part_acc, part_ml, heads, group, max_seq, n_splits,
+                     part_acc, part_ml, heads, max_seq, n_splits,
                      static_cast<int>(n_units), split_size, scale * kLog2e);
   int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
   if (rc != FA_OK) return rc;
@@ -909,43 +930,54 @@ int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
   return check_hip(hipGetLastError(), "decode_merge_kernel launch");
 }
 
+// Grouped queries: the matrix-core split pass, then the common merge.
+template <int D>
+int launch_group_decode(const void *q, const void *k_cache, const void *v_cache,
+                        const int32_t *seq_lens, void *o, bool out_f32, int batch, int heads,
+                        int kv_heads, int max_seq, float scale, int split_size,
+                        float *workspace, hipStream_t stream) {
+  const int group = heads / kv_heads;
+  const int nqg = group_queries(group);
+  const size_t n_qg = static_cast<size_t>(batch) * kv_heads * (group / nqg);
+  const int n_sp = (max_seq + split_size - 1) / split_size;
+  const size_t n_gu = n_qg * n_sp;
+  float *part_acc = workspace;
+  float *part_ml = workspace + static_cast<size_t>(batch) * heads * n_sp * D;
+  hipLaunchKernelGGL((decode_group_kernel<D>), dim3(static_cast<unsigned>(n_gu)), dim3(kWave),
+                     0, stream, static_cast<const _Float16 *>(q),
+                     static_cast<const _Float16 *>(k_cache),
+                     static_cast<const _Float16 *>(v_cache), seq_lens, part_acc, part_ml,
+                     heads, kv_heads, group, nqg, max_seq, n_sp, static_cast<int>(n_gu),
+                     split_size, scale * kLog2e);
+  int rc = check_hip(hipGetLastError(), "decode_group_kernel launch");
+  if (rc != FA_OK) return rc;
+  const unsigned n_bh = static_cast<unsigned>(static_cast<size_t>(batch) * heads);
+  if (out_f32)
+    hipLaunchKernelGGL((decode_merge_kernel<D, true>), dim3(n_bh), dim3(D), 0, stream,
+                       part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
+  else
+    hipLaunchKernelGGL((decode_merge_kernel<D, false>), dim3(n_bh), dim3(D), 0, stream,
+                       part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
+  return check_hip(hipGetLastError(), "decode_merge_kernel launch");
+}
+
 }  // namespace
 
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int kv_heads, int max_seq, int head_dim, float scale,
                   int split_size, bool auto_split, float *workspace, hipStream_t stream) {
-  const int group = heads / kv_heads;
+  if (heads != kv_heads) {
+    if (head_dim == 128)
+      return launch_group_decode<128>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads,
+                                      kv_heads, max_seq, scale, split_size, workspace, stream);
+    return launch_group_decode<64>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads,
+                                   kv_heads, max_seq, scale, split_size, workspace, stream);
+  }
   if (head_dim == 128)
     return launch_valu_decode<128>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads,
-                                   group, max_seq, scale, split_size, auto_split, workspace,
-                                   stream);
-  if (group > 1) {
-    // Grouped queries: the matrix-core split pass, then the common merge.
-    const int nqg = group_queries(group);
-    const size_t n_qg = static_cast<size_t>(batch) * kv_heads * (group / nqg);
-    const int n_sp = (max_seq + split_size - 1) / split_size;
-    const size_t n_gu = n_qg * n_sp;
-    float *part_acc = workspace;
-    float *part_ml = workspace + static_cast<size_t>(batch) * heads * n_sp * kHeadDim;
-    hipLaunchKernelGGL(decode_group_kernel, dim3(static_cast<unsigned>(n_gu)), dim3(kWave), 0,
-                       stream, static_cast<const _Float16 *>(q),
-                       static_cast<const _Float16 *>(k_cache),
-                       static_cast<const _Float16 *>(v_cache), seq_lens, part_acc, part_ml,
-                       heads, kv_heads, group, nqg, max_seq, n_sp, static_cast<int>(n_gu),
-                       split_size, scale * kLog2e);
-    int rc = check_hip(hipGetLastError(), "decode_group_kernel launch");
-    if (rc != FA_OK) return rc;
-    const unsigned n_bh = static_cast<unsigned>(static_cast<size_t>(batch) * heads);
-    if (out_f32)
-      hipLaunchKernelGGL((decode_merge_kernel<64, true>), dim3(n_bh), dim3(kHeadDim), 0, stream,
-                         part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
-    else
-      hipLaunchKernelGGL((decode_merge_kernel<64, false>), dim3(n_bh), dim3(kHeadDim), 0, stream,
-                         part_acc, part_ml, seq_lens, o, heads, max_seq, n_sp, split_size);
-    return check_hip(hipGetLastError(), "decode_merge_kernel launch");
-  }
-  return launch_valu_decode<64>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads, 1,
+                                   max_seq, scale, split_size, auto_split, workspace, stream);
+  return launch_valu_decode<64>(q, k_cache, v_cache, seq_lens, o, out_f32, batch, heads,
                                 max_seq, scale, split_size, auto_split, workspace, stream);
 }
 
@@ -958,13 +990,15 @@ int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
        reinterpret_cast<const void *>(decode_merge_kernel<64, false>), kHeadDim},
       {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<64, false>),
        kBhThreads},
-      {"decode_group_kernel", reinterpret_cast<const void *>(decode_group_kernel), kWave},
+      {"decode_group_kernel", reinterpret_cast<const void *>(decode_group_kernel<64>), kWave},
       {"decode_split_kernel<head_dim=128>",
        reinterpret_cast<const void *>(decode_split_kernel<128>), kSplitThreads},
       {"decode_merge_kernel<head_dim=128>",
        reinterpret_cast<const void *>(decode_merge_kernel<128, false>), 128},
       {"decode_bh_kernel<head_dim=128>",
        reinterpret_cast<const void *>(decode_bh_kernel<128, false>), kBhThreads},
+      {"decode_group_kernel<head_dim=128>",
+       reinterpret_cast<const void *>(decode_group_kernel<128>), kWave},
   };
   for (const K &k : ks) {
     if (*n < cap) {

@@ -41,8 +41,8 @@ int device_cu_count(int device);
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
                    bool out_f32, int batch, int heads, int kv_heads, int seq,
                    int head_dim, bool causal, float scale, hipStream_t stream);
-// head_dim is 64 or 128; grouped queries at head_dim 128 take the VALU
-// split-K / whole-sequence kernels with K/V head bh / group.
+// head_dim is 64 or 128; grouped queries take the matrix-core grouped pass
+// and the merge, the others the VALU split-K / whole-sequence kernels.
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int kv_heads, int max_seq, int head_dim, float scale,
@@ -53,7 +53,7 @@ int decode_units_per_row(int heads, int kv_heads);
 // Automatic chunk (cache rows per split) of the grouped-query decode pass:
 // the batch's max_seq-row work over the waves the GPU runs at once, in
 // multiples of 32 rows, at least 64.
-int decode_group_chunk(int batch, int units_per_row, int max_seq);
+int decode_group_chunk(int batch, int units_per_row, int max_seq, int head_dim);
 
 // Writes k_new / v_new ([B, H_kv, 1, 64]) at row seq_lens[b] of the caches
 // and advances seq_lens[b] (kv_cache.hip).

@@ -178,11 +178,10 @@ int resolve_split(int batch, int heads, int kv_heads, int max_seq, int head_dim,
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "decode split size must be >= 0, got %d", *split_size);
   if (*split_size == 0) {
-    // The matrix-core grouped pass (head_dim 64) has its own chunk policy;
-    // head_dim 128 decodes grouped queries with the per-head VALU kernels.
-    if (kv_heads != heads && head_dim == 64) {
-      *split_size =
-          decode_group_chunk(batch, decode_units_per_row(heads, kv_heads), max_seq);
+    // The matrix-core grouped pass has its own chunk policy.
+    if (kv_heads != heads) {
+      *split_size = decode_group_chunk(batch, decode_units_per_row(heads, kv_heads), max_seq,
+                                       head_dim);
       return FA_OK;
     }
     int dev = 0;

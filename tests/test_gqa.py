@@ -132,16 +132,16 @@ def _ragged_lens(batch, max_seq, seed):
     return lens
 
 
-def _decode_case(batch, heads, kv_heads, max_seq, seed):
+def _decode_case(batch, heads, kv_heads, max_seq, seed, d=64):
     lens = _ragged_lens(batch, max_seq, seed)
-    q = _rand((batch, heads, 1, 64), seed + 1)
-    k = _rand((batch, kv_heads, max_seq, 64), seed + 2)
-    v = _rand((batch, kv_heads, max_seq, 64), seed + 3)
+    q = _rand((batch, heads, 1, d), seed + 1)
+    k = _rand((batch, kv_heads, max_seq, d), seed + 2)
+    v = _rand((batch, kv_heads, max_seq, d), seed + 3)
     return q, k, v, lens
 
 
-def _run_decode(label, batch, heads, kv_heads, max_seq, seed, split=0):
-    q, k, v, lens = _decode_case(batch, heads, kv_heads, max_seq, seed)
+def _run_decode(label, batch, heads, kv_heads, max_seq, seed, split=0, d=64):
+    q, k, v, lens = _decode_case(batch, heads, kv_heads, max_seq, seed, d)
     ref = oracle.decode_gqa(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
     qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
     out32 = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE, split)
@@ -152,7 +152,11 @@ def _run_decode(label, batch, heads, kv_heads, max_seq, seed, split=0):
     torch.cuda.synchronize()
     _check(out16, out32, ref, label)
     diff = (out32 - rep).abs().max().item()
-    assert diff <= GROUPED_VS_REPEATED, f"{label}: {diff} from decode on the repeated caches"
+    # Both are within BOUND of the oracle; at head_dim 128 a row has twice
+    # the output elements, so the largest of the same per-element rounding
+    # differences is a little larger.
+    limit = GROUPED_VS_REPEATED * (2 if d == 128 else 1)
+    assert diff <= limit, f"{label}: {diff} from decode on the repeated caches"
     o = out32.cpu().numpy()
     assert not o[0].any()
     if batch > 1:
@@ -164,13 +168,14 @@ def _run_decode(label, batch, heads, kv_heads, max_seq, seed, split=0):
 GROUPS = [2, 3, 4, 5, 7, 8, 14, 16, 9, 32, 40, 48, 64]
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("group", GROUPS)
-def test_decode_gqa_groups(group):
-    """Every group size, on a small batch with ragged and edge lengths
-    (empty, negative, past the cache, 1, 63-65 rows)."""
+def test_decode_gqa_groups(group, d):
+    """Every group size at both head sizes, on a small batch with ragged and
+    edge lengths (empty, negative, past the cache, 1, 63-65 rows)."""
     kv_heads = 2 if group <= 16 else 1
-    _run_decode(f"B9 Hkv{kv_heads} G{group} L1500", 9, group * kv_heads, kv_heads, 1500,
-                seed=200 + group)
+    _run_decode(f"B9 Hkv{kv_heads} G{group} L1500 D{d}", 9, group * kv_heads, kv_heads, 1500,
+                seed=200 + group, d=d)
 
 
 @pytest.mark.parametrize("label,batch,heads,kv_heads,max_seq", [
@@ -180,15 +185,18 @@ def test_decode_gqa_groups(group):
     ("large batch, multi-query B300 H4 Hkv1 L120", 300, 4, 1, 120),
     ("long cache B2 H8 Hkv1 L20000", 2, 8, 1, 20000),
 ])
-def test_decode_gqa_shapes(label, batch, heads, kv_heads, max_seq):
-    _run_decode(label, batch, heads, kv_heads, max_seq, seed=400 + batch)
+@pytest.mark.parametrize("d", [64, 128])
+def test_decode_gqa_shapes(label, batch, heads, kv_heads, max_seq, d):
+    _run_decode(f"{label} D{d}", batch, heads, kv_heads, max_seq, seed=400 + batch, d=d)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("split", [4, 36, 64, 1000, 4096])
-def test_decode_gqa_forced_chunks(split):
+def test_decode_gqa_forced_chunks(split, d):
     """Forced chunk sizes (multiples of 4, not of the 32-row tile, larger
     than the cache) through the _decode_gqa_with_split hook."""
-    _run_decode(f"forced chunk {split} B4 H12 Hkv4 L2000", 4, 12, 4, 2000, seed=450, split=split)
+    _run_decode(f"forced chunk {split} B4 H12 Hkv4 L2000 D{d}", 4, 12, 4, 2000, seed=450,
+                split=split, d=d)
 
 
 def test_decode_gqa_negative_and_zero_scale():

@@ -360,7 +360,8 @@ def test_occupancy_report_rows():
                      "prefill_kernel<causal=false, head_dim=128>",
                      "decode_split_kernel", "decode_merge_kernel", "decode_bh_kernel",
                      "decode_group_kernel", "decode_split_kernel<head_dim=128>",
-                     "decode_merge_kernel<head_dim=128>", "decode_bh_kernel<head_dim=128>"]
+                     "decode_merge_kernel<head_dim=128>", "decode_bh_kernel<head_dim=128>",
+                     "decode_group_kernel<head_dim=128>"]
     for r in rows:
         assert set(r) == {"kernel", "threads_per_block", "registers_per_thread",
                           "shared_bytes_per_block", "max_active_blocks_per_sm",
