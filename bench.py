@@ -418,6 +418,59 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
+def cpu_per_config(budget_each=1.5):
+    """The CPU oracle on every BASELINE config (bounded samples, the same
+    inputs recipe as the GPU runs): whole configs where they are cheap (C1,
+    C4, C5), else a sample of heads timed for about `budget_each` seconds and
+    scaled to the config's head count (C2). Returns one row per config with
+    the CPU milliseconds per config and the rate in the config's unit."""
+    import numpy as np
+
+    from oracle import attention as orc
+
+    rows = []
+    for name, b, h, s, causal in [("C1 causal B1 H12 S128", 1, 12, 128, True),
+                                  ("C2 causal B4 H12 S1024", 4, 12, 1024, True),
+                                  ("C2 full B4 H12 S1024", 4, 12, 1024, False)]:
+        q, k, v = (t.numpy().astype(np.float32) for t in cpu_inputs_prefill(b, h, s))
+        qh, kh, vh = (x.reshape(b * h, s, 64) for x in (q, k, v))
+        orc.attention_cpu(qh[0], kh[0], vh[0], SCALE, causal)  # warm-up
+        t0 = time.perf_counter()
+        done = 0
+        while done < b * h or time.perf_counter() - t0 < budget_each:
+            i = done % (b * h)
+            orc.attention_cpu(qh[i], kh[i], vh[i], SCALE, causal)
+            done += 1
+            if done >= b * h and time.perf_counter() - t0 >= budget_each:
+                break
+            if done >= 4 * b * h:
+                break
+        per_head = (time.perf_counter() - t0) / done
+        ms = per_head * b * h * 1e3
+        rows.append({"config": name, "cpu_ms": ms,
+                     "cpu_tflops": attention_flops(b, h, s, causal) / (ms * 1e-3) / 1e12,
+                     "sample": f"{done} head-passes"})
+    for name, b, h, lmax, lens in [("C4 decode B1 H12 L4096", 1, 12, 4096, [4096]),
+                                   ("C5 ragged decode B32 H14 Lmax4096", 32, 14, 4096, None)]:
+        import torch
+
+        q, k, v, rl = cpu_inputs_decode(b, h, lmax)
+        if lens is not None:
+            rl = torch.tensor(lens, dtype=torch.int32)
+        qn, kn, vn, ln = (x.numpy() for x in (q.float(), k.float(), v.float(), rl))
+        orc.decode(qn, kn, vn, ln, SCALE)  # warm-up
+        t0 = time.perf_counter()
+        runs = 0
+        while runs < 1 or (time.perf_counter() - t0 < budget_each and runs < 20):
+            orc.decode(qn, kn, vn, ln, SCALE)
+            runs += 1
+        ms = (time.perf_counter() - t0) / runs * 1e3
+        nbytes = decode_bytes(h, rl, lmax)
+        rows.append({"config": name, "cpu_ms": ms, "cpu_gbs": nbytes / (ms * 1e-3) / 1e9,
+                     "sample": f"{runs} whole-config runs"})
+    return rows
+
+
 def copy_calibration(steps):
     """A plain 1 GiB device-to-device copy, `steps` times: the known-size
     kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters into HBM
@@ -600,6 +653,22 @@ def main():
         cb = cpu_baseline()
         result["cpu_baseline"] = cb
         log(f"  {cb['value'] * 1e3:.2f} GFLOP/s on {cb['cores']} threads")
+        if args.only == "all":
+            log("CPU oracle on every config (bounded samples) ...")
+            per = cpu_per_config()
+            # Config 3 comes from the main baseline sample above.
+            per.insert(3, {"config": "C3 causal B1 H14 S4096",
+                           "cpu_ms": cb["seconds_per_head"] * 14 * 1e3,
+                           "cpu_tflops": cb["value"], "sample": "the cpu_baseline sample"})
+            cb["per_config"] = per
+            by_name = {r["config"]: r for r in per}
+            for row in result.get("configs", []):
+                c = by_name.get(row["config"])
+                if c:
+                    row["cpu_ms"] = c["cpu_ms"]
+                    row["gpu_speedup_over_cpu"] = c["cpu_ms"] / row["ms"]
+            for r in per:
+                log(f"  {r['config']}: {r['cpu_ms']:.2f} ms on the CPU ({r['sample']})")
 
     print(json.dumps(result), flush=True)
 
