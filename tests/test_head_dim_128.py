@@ -179,3 +179,53 @@ def test_head_dim_mismatches_are_rejected():
     bad = torch.randn(1, 2, 8, 96, device="cuda").half()
     with pytest.raises(RuntimeError, match="head_dim"):
         flashattn_cuda.prefill(bad, bad, bad, True, SCALE)
+
+
+# ---------------------------------------------------------------------------
+# The head-size entry points of the C ABI, called directly (ctypes)
+# ---------------------------------------------------------------------------
+
+
+def _capi():
+    import ctypes
+    import os
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(flashattn_cuda.__file__),
+                                   "libflashattn_hip.so"))
+    lib.fa_last_error.restype = ctypes.c_char_p
+    lib.fa_decode_hd_workspace_bytes.restype = ctypes.c_size_t
+    return lib
+
+
+def test_capi_prefill_hd_and_decode_hd_match_python_api():
+    import ctypes
+
+    lib = _capi()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 6, 300, D, generator=g).half().cuda()
+    k = torch.randn(2, 3, 300, D, generator=g).half().cuda()
+    v = torch.randn(2, 3, 300, D, generator=g).half().cuda()
+    o = torch.empty_like(q)
+    rc = lib.fa_prefill_hd(ptr(q), ptr(k), ptr(v), ptr(o), 0, 2, 6, 3, 300, D, 1,
+                           ctypes.c_float(SCALE), None, ctypes.c_size_t(0), stream)
+    assert rc == 0, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(o, flashattn_cuda.prefill_gqa(q, k, v, True, SCALE))
+
+    qd = torch.randn(2, 6, 1, D, generator=g).half().cuda()
+    lens = torch.tensor([300, 17], dtype=torch.int32, device="cuda")
+    for kv_heads, kc, vc in ((3, k, v), (6, q, q)):
+        od = torch.empty_like(qd)
+        ws_bytes = lib.fa_decode_hd_workspace_bytes(2, 6, kv_heads, 300, D, 0)
+        assert ws_bytes > 0, lib.fa_last_error()
+        ws = torch.empty(ws_bytes // 4 + 4, dtype=torch.float32, device="cuda")
+        rc = lib.fa_decode_hd(ptr(qd), ptr(kc), ptr(vc), ptr(lens), ptr(od), 0, 2, 6, kv_heads,
+                              300, D, ctypes.c_float(SCALE), 0, ptr(ws),
+                              ctypes.c_size_t(ws_bytes), stream)
+        assert rc == 0, lib.fa_last_error()
+        torch.cuda.synchronize()
+        want = (flashattn_cuda.decode_gqa(qd, kc, vc, lens, SCALE) if kv_heads != 6 else
+                flashattn_cuda.decode(qd, kc, vc, lens, SCALE))
+        assert torch.equal(od, want)
