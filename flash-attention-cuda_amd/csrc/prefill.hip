@@ -34,6 +34,11 @@
 //            5-stage V ring of 64-key tiles, all row-major with 16-byte
 //            chunks XOR-swizzled per row, filled by direct global->LDS loads
 //            (global_load_lds_dwordx4) four tiles ahead of use.
+//   head_dim 128: the same block, pipeline and rules with 32-key tiles of
+//            256-byte rows (still 8 KiB, still 16 MFMAs per step), Q^T loaded
+//            from HBM straight into registers instead of through LDS, and
+//            two masked tiles per key half on the causal diagonal (the second
+//            one takes the plain per-tile step). Constants in Geo<D>.
 //
 // Main loop (tiles that need no mask), per wave and step k of its half:
 //   wait for tile k+2 -> barrier -> issue the loads of tile k+4 ->

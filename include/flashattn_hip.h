@@ -6,7 +6,8 @@
  * has no torch types, so ctypes, cgo, JNI or a C++ host can bind it directly.
  * The Python package `flashattn_cuda` wraps it with the reference's
  * pybind11 surface (`prefill`, `decode`, `_decode_with_split`,
- * `choose_decode_split`, `occupancy_report`, `head_dim`).
+ * `choose_decode_split`, `occupancy_report`, `head_dim`, `legacy_naive`,
+ * `legacy_tiled`, `legacy_fused`).
  *
  * Reference interface that each entry point replaces
  * (paths relative to shrvan30/flash-attention-cuda):
@@ -46,7 +47,10 @@
  * Tensor layout (same as the reference): q, k, v, o are [B, H, S, 64]
  * contiguous fp16 (IEEE binary16); a decode cache is [B, H, Lmax, 64]; the
  * decode query and output are [B, H, 1, 64]; seq_lens is [B] int32 in device
- * memory. Every pointer must be a device pointer aligned to 16 bytes.
+ * memory. The *_hd entry points take the head size (64 or 128) as an
+ * argument and the same layouts with that last dimension; the legacy entry
+ * point takes (n, 64) fp32 rows. Every pointer must be a device pointer
+ * aligned to 16 bytes.
  *
  * Launches are asynchronous on `stream` (a hipStream_t; NULL is the default
  * stream) and never synchronise the host. A non-zero return value is an
@@ -90,7 +94,8 @@ typedef struct fa_occupancy_entry {
 /* Library version string, e.g. "2.0.0-gfx950". */
 const char *fa_version(void);
 
-/* The head size every kernel is specialised for: 64. */
+/* The reference's head size, 64 (the entry points without a head_dim
+ * argument use it; the *_hd ones also take 128). */
 int fa_head_dim(void);
 
 /* Message describing the last failure on the calling thread ("" if none). */
