@@ -310,7 +310,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(
     const float *__restrict__ part_acc, const float *__restrict__ part_ml,
     const int32_t *__restrict__ seq_lens, void *__restrict__ o, int heads,
     int max_seq, int n_splits, int chunk) {
-  constexpr int kBatch = 8;  // chunks whose partial rows are loaded together
+  constexpr int kBatch = 16;  // chunks whose partial rows are loaded together
   const int bh = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
   const int dim = threadIdx.x;

@@ -356,7 +356,10 @@ struct HalfRing {
   // visible to the whole block, then the loads of tile k + 4 are issued.
   // Its K stage last held tile k, its V stage tile k - 1: the main loop read
   // them at the end of steps k - 2 and k - 1, the masked step reads a tile
-  // before its own barrier.
+  // before its own barrier. Each wave drains its LDS reads (lgkmcnt(0))
+  // before the barrier: a V read issued just before it could otherwise still
+  // sit in the LDS queue when another wave's refill of that stage lands
+  // (measured cost: none, the reads are needed right after anyway).
   // A plain s_barrier: __syncthreads() would add a release fence, which
   // drains every outstanding load of the ring.
   __device__ __forceinline__ void advance(int k) const {
@@ -364,6 +367,7 @@ struct HalfRing {
       wait_loads<kLoadsPerTile>();
     else
       wait_loads<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     issue(k + kAhead);
   }
