@@ -30,11 +30,14 @@
 //    row group (no LDS, no ds_bpermute).
 //  * The softmax runs in the log2 domain: each score is multiplied by
 //    scale * log2(e), so p = exp2(s - m) maps to one v_exp_f32.
-//  * Grouped-query attention (H_kv < H K/V heads): a unit holds NQ query
-//    heads of one K/V head (NQ the largest divisor of H / H_kv up to 8), so
-//    each cache row is loaded once for all of them.
-//  * The per-lane online-softmax states are merged across the 8 row groups
-//    of the wave with shuffles, and across chunks by the merge kernel.
+//  * head_dim 128 keeps the lane -> 16 B mapping: 16 lanes per row, 4 rows
+//    per load instruction, a 4-step DPP sum (RowGeo<D>).
+//  * The per-lane online-softmax states are merged across the row groups of
+//    the wave with shuffles, and across chunks by the merge kernel.
+//  * Grouped-query attention (H_kv < H K/V heads) does not use these VALU
+//    passes: decode_group_kernel (below) runs the split pass on the matrix
+//    cores with up to 32 query heads of one K/V head per wave, so each cache
+//    row is loaded once for all of them, and shares the merge kernel.
 //
 // Partial results are stored with m in the log2 domain; only this file
 // produces and consumes them.
