@@ -1,8 +1,8 @@
 // MFMA tile building blocks shared by the gfx950 attention kernels
 // (prefill.hip, decode.hip): the 16-byte-chunk swizzles of a row-major
-// [rows x 64] (or [rows x 128]) fp16 tile in LDS, direct global->LDS loads, the fragment
-// offsets of v_mfma_f32_32x32x16_f16 operands read from such a tile, and the
-// lane-pair max of an S^T accumulator.
+// [rows x 64] or [rows x 128] fp16 tile in LDS, direct global->LDS loads, the
+// fragment offsets of v_mfma_f32_32x32x16_f16 operands read from such a tile,
+// and the lane-pair max of an S^T accumulator.
 //
 // Operand conventions (lane l: column l % 32, half g = l / 32):
 //   S^T = K Q^T : A = 32 key rows x 16 head dims, B = 16 head dims x 32

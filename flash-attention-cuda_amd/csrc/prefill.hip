@@ -1,4 +1,4 @@
-// Causal / full FlashAttention prefill for head_dim 64 on gfx950 MFMA.
+// Causal / full FlashAttention prefill for head_dim 64 (and 128) on gfx950 MFMA.
 //
 // Reference behaviour: prefill_kernel<CAUSAL> and launch_prefill in
 // csrc/prefill.cu:164-373 of shrvan30/flash-attention-cuda (online softmax
@@ -41,7 +41,8 @@
 //            one takes the plain per-tile step). Constants in Geo<D>.
 //
 // Main loop (tiles that need no mask), per wave and step k of its half:
-//   wait for tile k+2 -> barrier -> issue the loads of tile k+4 ->
+//   wait for tile k+2 and this wave's LDS reads -> barrier -> issue the loads
+//   of tile k+4 ->
 //   O *= alpha_{k-1} (only where a row's max rose) -> row max of S_k ->
 //   { QK(k+1) and PV(k-1) on the matrix cores } interleaved with
 //   { exp / pack / row sum of S_k on the VALU } ->
