@@ -16,8 +16,9 @@
 //
 // Split path details, laid out for CDNA4:
 //
-//  * One WAVE owns one (b, h, chunk) unit; a block is four independent waves
-//    (no LDS, no barrier). Chunks past a sequence's end exit at once.
+//  * One WAVE owns one (b, h, chunk) unit; a block is one wave (grids of up
+//    to 2 x CUs units) or four independent waves (no LDS, no barrier).
+//    Chunks past a sequence's end exit at once.
 //  * A wave reads 8 cache rows per load instruction: lane = 8 * row + slice,
 //    each lane owns 8 head dims (16 B), so one wave64 load moves 1 KiB of
 //    contiguous cache and every row is one 128 B segment. The loads are
@@ -207,7 +208,7 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
 // Pass 1 (decode.cu:50-138): one wave folds cache rows
 // [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
 // partial (m, l, acc[D]). Unit u = chunk_i * (B * H) + (b * H + h) is
-// handled by wave u % 4 of block u / 4.
+// handled by wave u % W of block u / W, W = blockDim.x / 64 (1 or 4).
 template <int D>
 __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
     float *__restrict__ part_acc, float *__restrict__ part_ml, int heads,
     int max_seq, int n_splits, int n_units, int chunk, float qscale) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int unit = static_cast<int>(blockIdx.x) * kSplitWaves +
+  const int unit = static_cast<int>(blockIdx.x * (blockDim.x / kWave)) +
                    __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   if (unit >= n_units) return;
   // Chunk-major order: every (b, h)'s first chunk is dispatched first, its
@@ -908,17 +909,26 @@ int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
   float *part_acc = workspace;
   float *part_ml = workspace + bh * n_splits * D;
   const size_t n_units = bh * n_splits;
+  // Up to 2 x CUs units (the chunk chooser's own target), one-wave blocks
+  // put the units on every CU instead of a quarter of them (measured per
+  // call: B1 H12 L4096 8.2 against 8.5 us, B2 H8 L16384 18.7 against 21.5);
+  // above that, four-wave blocks (B4 H12 L4096: 13.3 against 14.9 us).
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != FA_OK) return rc;
+  const int waves_per_block =
+      n_units <= 2 * static_cast<size_t>(device_cu_count(dev)) ? 1 : kSplitWaves;
   const unsigned split_blocks =
-      static_cast<unsigned>((n_units + kSplitWaves - 1) / kSplitWaves);
+      static_cast<unsigned>((n_units + waves_per_block - 1) / waves_per_block);
 
   hipLaunchKernelGGL((decode_split_kernel<D>), dim3(split_blocks),
-                     dim3(kSplitThreads), 0, stream,
+                     dim3(waves_per_block * kWave), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k_cache),
                      static_cast<const _Float16 *>(v_cache), seq_lens,
                      part_acc, part_ml, heads, max_seq, n_splits,
                      static_cast<int>(n_units), split_size, scale * kLog2e);
-  int rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
+  rc = check_hip(hipGetLastError(), "decode_split_kernel launch");
   if (rc != FA_OK) return rc;
 
   if (out_f32) {
