@@ -51,8 +51,9 @@
 //   S and P are double-buffered (the loop is unrolled by two), so the MFMAs of
 //   a step never wait for that step's softmax. The one tile per half that
 //   needs a mask (causal diagonal, ragged tail) is the pipeline's last step,
-//   with a masked softmax. Blocks whose query rows see fewer than 256 keys
-//   take a plain per-tile step with split P instead.
+//   with a masked softmax. Blocks whose query rows see fewer than 256 keys,
+//   and every block when the logits are wide (|scale| sqrt(D) > 1.5), take a
+//   plain per-tile step with split P instead.
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
@@ -97,6 +98,8 @@ constexpr int kVStages = 5;
 constexpr int kAhead = 4;                     // tiles in flight ahead of use
 constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per tile
 constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split P
+// |scale| * sqrt(D) above this (1 is the standard 1/sqrt(D)): split P on every row.
+constexpr float kSplitAllWidth = 1.5f;
 constexpr float kNegHuge = -3.0e38f;
 
 // Tile geometry for head_dim D (64 or 128). A K or V tile is always 8 KiB:
@@ -422,7 +425,7 @@ template <int D, bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
-    int n_qtiles, int group, float c_scale, bool negate_q) {
+    int n_qtiles, int group, float c_scale, bool negate_q, bool split_all) {
   using G = Geo<D>;
   constexpr int kBc = G::kBc;
   constexpr int kKB = G::kKB;
@@ -483,7 +486,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // whenever n_main > 0: causal, the diagonal adds two tiles; full, the
   // ragged tail one). Blocks with short rows take the plain split-P step on
   // every tile.
-  const bool short_rows = CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow;
+  const bool short_rows =
+      split_all || (CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow);
   const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
@@ -708,7 +712,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
 template <int D, bool CAUSAL, bool OUT_F32>
 void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
-                int seq, int group, float c_scale, bool negate_q, hipStream_t stream) {
+                int seq, int group, float c_scale, bool negate_q, bool split_all,
+                hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
   const unsigned blocks = static_cast<unsigned>(bh) * n_qtiles;
   hipLaunchKernelGGL((prefill_kernel<D, CAUSAL, OUT_F32>), dim3(blocks),
@@ -716,25 +721,29 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
                      static_cast<const _Float16 *>(v), o, seq, n_qtiles, group,
-                     c_scale, negate_q);
+                     c_scale, negate_q, split_all);
 }
 
 }  // namespace
 
 template <int D>
 void launch_d(const void *q, const void *k, const void *v, void *o, bool out_f32, int bh,
-              int seq, int group, bool causal, float c_scale, bool negate_q,
+              int seq, int group, bool causal, float c_scale, bool negate_q, bool split_all,
               hipStream_t stream) {
   if (causal) {
     if (out_f32)
-      launch_one<D, true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+      launch_one<D, true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
+                                stream);
     else
-      launch_one<D, true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+      launch_one<D, true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
+                                 stream);
   } else {
     if (out_f32)
-      launch_one<D, false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+      launch_one<D, false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
+                                 stream);
     else
-      launch_one<D, false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, stream);
+      launch_one<D, false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
+                                  stream);
   }
 }
 
@@ -745,10 +754,17 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
   const int group = heads / kv_heads;
   const float c_scale = fabsf(scale) * kLog2e;
   const bool negate_q = scale < 0.f;
+  // Logits much wider than N(0,1) at 1/sqrt(D) make rows peaky at any length,
+  // where one fp16 rounding of P costs up to ~5e-4 (measured: D = 128 at
+  // scale 0.3, 3.4x the standard width): every row then takes the split-P
+  // step.
+  const bool split_all = fabsf(scale) * sqrtf(static_cast<float>(head_dim)) > kSplitAllWidth;
   if (head_dim == 128)
-    launch_d<128>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, stream);
+    launch_d<128>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, split_all,
+                  stream);
   else
-    launch_d<64>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, stream);
+    launch_d<64>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, split_all,
+                 stream);
   return check_hip(hipGetLastError(), "prefill_kernel launch");
 }
 

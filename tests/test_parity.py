@@ -185,6 +185,21 @@ def test_negative_and_large_scales():
         assert np.abs(out.cpu().numpy() - ref).max() <= BOUND, scale
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("scale", [0.3, -0.3, 1.0])
+def test_wide_logits_long_rows_stay_in_bound(d, causal, scale):
+    """Logits several times wider than N(0,1) at 1/sqrt(D) make rows peaky at
+    any length (one fp16 rounding of P measured up to ~5e-4 there); with
+    |scale| * sqrt(D) > 1.5 the launcher splits P on every row, long rows
+    (up to 1100 keys) included."""
+    q, k, v = oracle.make_prefill_inputs(1, 3, 1100, seed=41, head_dim=d)
+    ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, scale)
+    out32 = flashattn_cuda._prefill_fp32(q.cuda(), k.cuda(), v.cuda(), causal, scale)
+    out16 = flashattn_cuda.prefill(q.cuda(), k.cuda(), v.cuda(), causal, scale)
+    _check(out16, out32, ref, f"wide logits D{d} causal={causal} scale={scale}")
+
+
 def test_decode_equals_prefill_rows_at_full_size():
     """Every position t of a long causal prefill equals decode at len t+1."""
     q, k, v = oracle.make_prefill_inputs(2, 14, 4096, seed=10)
