@@ -415,6 +415,8 @@ struct GroupGeo {
 };
 
 constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
+// Wide logits, |scale| sqrt(D) > 1.5, in the log2 domain of qscale.
+constexpr float kGroupWideLog2 = 1.5f * kLog2e;
 
 // Online softmax and O^T += V^T P^T for one tile whose S^T (raw q.k) is in
 // `sacc`: m is the running max in the log2 domain (scores times c), l this
@@ -572,7 +574,9 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
 
   // The last tile is partial when the chunk's row count is not a multiple of
   // 32: only that tile is masked. Sequences shorter than kGroupSplitPBelow
-  // rows get the split (hi + lo) P product on every tile.
+  // rows, and every sequence when the logits are wide (|scale| sqrt(D) >
+  // 1.5, the prefill's rule: peaky rows at any length), get the split
+  // (hi + lo) P product on every tile.
   const bool partial_tail = ((end - begin) & (kGroupTile - 1)) != 0;
   auto run = [&](auto split_tag) {
     constexpr bool SPLIT = decltype(split_tag)::value;
@@ -624,7 +628,8 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
       }
     }
   };
-  if (len < kGroupSplitPBelow)
+  const bool wide = qscale * qscale * static_cast<float>(D) > kGroupWideLog2 * kGroupWideLog2;
+  if (len < kGroupSplitPBelow || wide)
     run(std::true_type{});
   else
     run(std::false_type{});

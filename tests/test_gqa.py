@@ -208,6 +208,21 @@ def test_decode_gqa_negative_and_zero_scale():
         assert np.abs(out - ref).max() <= BOUND, scale
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("scale", [0.3, -0.3, 1.0])
+def test_decode_gqa_wide_logits_long_rows(d, scale):
+    """Logits several times wider than N(0,1) at 1/sqrt(D) make rows peaky at
+    any length; with |scale| * sqrt(D) > 1.5 the grouped pass splits P on
+    every tile, long caches (up to 3000 rows) included."""
+    q, k, v, _ = _decode_case(4, 14, 2, 3000, seed=470, d=d)
+    lens = torch.tensor([3000, 2100, 700, 257], dtype=torch.int32)
+    ref = oracle.decode_gqa(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), scale)
+    out = flashattn_cuda._decode_gqa_fp32(q.cuda(), k.cuda(), v.cuda(), lens.cuda(), scale)
+    err = float(np.abs(out.cpu().numpy() - ref).max())
+    print(f"[decode_gqa wide logits D{d} scale={scale}] fp32-out err {err:.3e}")
+    assert err <= BOUND, err
+
+
 def test_decode_gqa_c5_shape():
     """The C5 batch (B32 H14 Lmax4096, ragged) with 2 K/V heads (group 7)."""
     q, k, v, lens = oracle.make_decode_inputs(32, 14, 4096, seed=0)
