@@ -52,8 +52,10 @@
 //   a step never wait for that step's softmax. The one tile per half that
 //   needs a mask (causal diagonal, ragged tail) is the pipeline's last step,
 //   with a masked softmax. Blocks whose query rows see fewer than 256 keys,
-//   and every block when the logits are wide (|scale| sqrt(D) > 1.5), take a
-//   plain per-tile step with split P instead.
+//   and every block when the scale alone makes the logits wide
+//   (|scale| sqrt(D) > 1.5), take a plain per-tile step with split P instead;
+//   so does a second pass over any other block whose rows turn out peaky
+//   (softmax paragraph below).
 //
 // Products (v_mfma_f32_32x32x16_f16, lane l: column l % 32, half g = l / 32)
 //   S^T = K Q^T : A = K rows (ds_read_b128), B = Q^T fragments resident in
@@ -76,11 +78,21 @@
 // running max, so the dominant key of a row always enters the PV product as
 // P = 1 exactly. The row sum l is accumulated from the same fp16 P values the
 // PV product consumes (v_dot2_f32_f16), so the weights that multiply V sum to
-// exactly the l they are divided by. For query rows that see fewer than 256
-// keys, P is split into hi + lo fp16 parts and the PV product is issued
-// twice: those rows have few, large weights, where one fp16 rounding of P
-// would cost up to ~4e-4 of output accuracy (measured with one rounding: 8e-5
-// at >= 256 keys, 1.2e-4 at >= 128 keys).
+// exactly the l they are divided by.
+//
+// Precision of P: one fp16 rounding of each weight w = p / l moves an output
+// row by about 2^-11 sqrt(sum w^2) times the spread of V, summed over the
+// rounded weights (the P = 1 key is exact and does not count). Rows carried by
+// a few keys therefore need P split into hi + lo fp16 parts, with the PV
+// product issued twice (relative error ~2^-22). Rows that see fewer than 256
+// keys always take the split. Every other row tracks an upper bound of its
+// rounded mass r = sum w^2: per tile, (largest weight) x (weight sum), minus
+// the exact 1 of a tile that sets the running max, rescaled with the max like
+// l. A block with a row whose r / l^2 ends above kRedoRoundedMassAbove (0.08:
+// output error ~2e-4 at the bound, measured on inputs up to 3.4x the N(0,1)
+// logit width) is computed again with split P on every tile. Independent
+// N(0,1) inputs at 1/sqrt(D) stay below 0.065 (rows with 256-383 keys) and
+// below 0.045 beyond, so they take the single-rounding pass only.
 
 #include "fa_internal.h"
 #include "mfma_tile.h"
@@ -98,7 +110,13 @@ constexpr int kVStages = 5;
 constexpr int kAhead = 4;                     // tiles in flight ahead of use
 constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per tile
 constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split P
-// |scale| * sqrt(D) above this (1 is the standard 1/sqrt(D)): split P on every row.
+// A block is recomputed with split P when, for one of its rows, the squared
+// normalised weights that took a single fp16 rounding sum to more than this
+// (bounded per tile by the tile's largest weight times its weight sum; see the
+// precision note at the top of the file).
+constexpr float kRedoRoundedMassAbove = 0.08f;
+// |scale| * sqrt(D) above this (1 is the standard 1/sqrt(D)): rows are peaky
+// from the scale alone, so the first (single-rounding) pass is skipped.
 constexpr float kSplitAllWidth = 1.5f;
 constexpr float kNegHuge = -3.0e38f;
 
@@ -124,8 +142,8 @@ struct Geo {
   static constexpr int kQHalves = kQInLds ? kBr * D : 0;                  // 16 KiB / 0
   static constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
   static constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 / 144 KiB
-  // Half-merge exchange at the end: [row wave][O^T values, m, l][64 lanes] fp32.
-  static constexpr int kXchg = 16 * kDB + 2;
+  // Half-merge exchange at the end: [row wave][O^T values, m, l, r][64 lanes] fp32.
+  static constexpr int kXchg = 16 * kDB + 3;
   static_assert(kRowWaves * kXchg * kWave * 4 <= kLdsHalves * 2, "exchange fits in LDS");
 };
 
@@ -138,6 +156,8 @@ template <int D>
 struct SoftmaxState {
   float m;                      // running max (log2 domain, already scaled by c)
   float l;                      // this lane's share of the row sum
+  float r;                      // this lane's share of the rounded mass (below)
+  float pm;                     // largest weight of the current tile
   floatx16 o[Geo<D>::kDB];      // O^T accumulators, one per 32-dim block
 };
 
@@ -223,14 +243,27 @@ __device__ __forceinline__ float tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, f
     }
   }
   mx = max_lane_pair(mx);
-  const float m_new = fmaxf(st.m, mx * c_scale);
-  const float alpha = fast_exp2(st.m - m_new);
+  float mx_c, m_new, alpha;
+  {
+    // No contraction here: with mx_c rounded once, a tile that sets the
+    // running max gets largest weight exp2(0) = 1 exactly.
+#pragma clang fp contract(off)
+    mx_c = mx * c_scale;
+    m_new = fmaxf(st.m, mx_c);
+    alpha = fast_exp2(st.m - m_new);
+    st.pm = fast_exp2(mx_c - m_new);
+  }
   st.m = m_new;
   st.l *= alpha;
+  st.r *= alpha * alpha;
   return alpha;
 }
 
-// P^T fragments (hi [+ lo]) of one tile and the row-sum update.
+// P^T fragments (hi [+ lo]) of one tile and the row-sum update. Without the
+// lo part, the rounded mass r grows by (largest weight) x (weight sum) of the
+// tile, an upper bound on the tile's squared weights; a weight equal to the
+// running max is exactly 1 in fp16 and is left out (half of it in each lane
+// of the pair, since only their sum is used).
 template <bool MASK, bool SPLIT, int D>
 __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float c_scale,
                                          SoftmaxState<D> &st, half8 (&p_hi)[Geo<D>::kKS],
@@ -264,6 +297,7 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float
     }
   }
   st.l += lsum;
+  if (!SPLIT) st.r = fmaf(-0.5f, floorf(st.pm), fmaf(st.pm, lsum, st.r));
 }
 
 // O *= alpha when the max of any row of the wave rose (wave-uniform branch;
@@ -486,61 +520,119 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // whenever n_main > 0: causal, the diagonal adds two tiles; full, the
   // ragged tail one). Blocks with short rows take the plain split-P step on
   // every tile.
-  const bool short_rows =
-      split_all || (CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow);
+  const bool static_split = CAUSAL ? q0 < kSplitPRowsBelow : seq < kSplitPRowsBelow;
+  // Pass 0 rounds P to fp16 once on rows that see enough keys; blocks whose
+  // row sums then show a peaky row run again with split P on every tile.
+  const bool short_rows = split_all || static_split;
   const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
 
-  // Q: for D = 64 the tile goes to LDS (16 row blocks of 8 rows, 2 per wave;
-  // K swizzle); for D = 128 each lane loads its Q^T fragments (query my_q,
-  // head dims [64 g + 8 s, +8)) straight into registers. Then this half's
-  // first kAhead tiles.
   const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
   half8 qf[kDS];
-  if constexpr (G::kQInLds) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int rblock = 2 * wave + i;
-      const int r = rblock * 8 + (lane >> 3);
-      const int row = min(q0 + r, seq - 1);
-      global_to_lds16(q + head_off + static_cast<size_t>(row) * D +
-                          (((lane & 7) ^ k_swz(r)) << 3),
-                      q_lds + rblock * 8 * D);
-    }
-  } else {
-    const _Float16 *qrow = q + head_off + static_cast<size_t>(min(my_q, seq - 1)) * D +
-                           (lane >> 5) * (D / 2);
-#pragma unroll
-    for (int s = 0; s < kDS; ++s) qf[s] = *reinterpret_cast<const half8 *>(qrow + 8 * s);
-  }
-#pragma unroll
-  for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
-  // Q and tiles 0, 1 resident (tiles 2, 3 may still be in flight; the first
-  // advance waits for tile 2).
-  if (ring.exists(3))
-    wait_loads<2 * kLoadsPerTile>();
-  else if (ring.exists(2))
-    wait_loads<kLoadsPerTile>();
-  else
-    wait_loads<0>();
-  __builtin_amdgcn_s_barrier();
-
-  // Q^T fragments: lane holds query my_q, head dims [(D / 2) g + 8 s, +8).
-#pragma unroll
-  for (int s = 0; s < kDS; ++s) {
-    if constexpr (G::kQInLds) qf[s] = lds_b128(q_lds + rw * kRowsPerWave * D + fo.k[s]);
-    if (negate_q) qf[s] = -qf[s];
-  }
-
   SoftmaxState<D> st;
-  st.m = kNegHuge;
-  st.l = 0.f;
+  auto prologue = [&]() {
+    // Q: for D = 64 the tile goes to LDS (16 row blocks of 8 rows, 2 per wave;
+    // K swizzle); for D = 128 each lane loads its Q^T fragments (query my_q,
+    // head dims [64 g + 8 s, +8)) straight into registers. Then this half's
+    // first kAhead tiles.
+    if constexpr (G::kQInLds) {
 #pragma unroll
-  for (int db = 0; db < kDB; ++db)
+      for (int i = 0; i < 2; ++i) {
+        const int rblock = 2 * wave + i;
+        const int r = rblock * 8 + (lane >> 3);
+        const int row = min(q0 + r, seq - 1);
+        global_to_lds16(q + head_off + static_cast<size_t>(row) * D +
+                            (((lane & 7) ^ k_swz(r)) << 3),
+                        q_lds + rblock * 8 * D);
+      }
+    } else {
+      const _Float16 *qrow = q + head_off + static_cast<size_t>(min(my_q, seq - 1)) * D +
+                             (lane >> 5) * (D / 2);
 #pragma unroll
-    for (int a = 0; a < 16; ++a) st.o[db][a] = 0.f;
+      for (int s = 0; s < kDS; ++s) qf[s] = *reinterpret_cast<const half8 *>(qrow + 8 * s);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kAhead; ++kk) ring.issue(kk);
+    // Q and tiles 0, 1 resident (tiles 2, 3 may still be in flight; the first
+    // advance waits for tile 2).
+    if (ring.exists(3))
+      wait_loads<2 * kLoadsPerTile>();
+    else if (ring.exists(2))
+      wait_loads<kLoadsPerTile>();
+    else
+      wait_loads<0>();
+    __builtin_amdgcn_s_barrier();
 
+    // Q^T fragments: lane holds query my_q, head dims [(D / 2) g + 8 s, +8).
+#pragma unroll
+    for (int s = 0; s < kDS; ++s) {
+      if constexpr (G::kQInLds) qf[s] = lds_b128(q_lds + rw * kRowsPerWave * D + fo.k[s]);
+      if (negate_q) qf[s] = -qf[s];
+    }
+
+    st.m = kNegHuge;
+    st.l = 0.f;
+    st.r = 0.f;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) st.o[db][a] = 0.f;
+  };
+  auto split_steps = [&](int kk0) {
+    // ---- short-row blocks: one plain split-P step per tile ---------------------
+    // Tile kk is resident (waited for by an earlier advance, or by the
+    // prologue); its fragments are read before the barrier that lets the load
+    // of tile kk + 4 overwrite its K stage.
+    for (int kk = kk0; kk < n_steps; ++kk) {
+      const int key0 = ring.tile(kk) * kBc;
+      const bool active = key0 < wave_key_end;
+      KFrags<D> kf;
+      VFrags<D> vf;
+      if (active) {
+        read_k(ring.kstage(kk), fo, kf);
+        read_v(ring.vstage(kk), fo, vf);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done
+      ring.advance(kk);
+      if (active) slow_step<CAUSAL, D>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
+    }
+  };
+  auto merge_halves = [&]() -> float * {
+    // ---- merge the two halves through LDS, normalise, store ------------------
+    // Layout: [row wave][kXchg values][64 lanes] fp32 from the start of LDS. Every
+    // load the ring issued has completed; the barrier ends every read of it.
+    wait_loads<0>();
+    __builtin_amdgcn_s_barrier();
+    float *xchg = reinterpret_cast<float *>(lds) + rw * (G::kXchg * kWave) + lane;
+    if (half == 1) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) xchg[(16 * db + a) * kWave] = st.o[db][a];
+      xchg[16 * kDB * kWave] = st.m;
+      xchg[(16 * kDB + 1) * kWave] = st.l;
+      xchg[(16 * kDB + 2) * kWave] = st.r;
+    }
+    __syncthreads();
+    if (half == 0) {
+      const float m1 = xchg[16 * kDB * kWave];
+      const float l1 = xchg[(16 * kDB + 1) * kWave];
+      const float m = fmaxf(st.m, m1);
+      const float f0 = fast_exp2(st.m - m);
+      const float f1 = fast_exp2(m1 - m);
+#pragma unroll
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a)
+          st.o[db][a] = st.o[db][a] * f0 + xchg[(16 * db + a) * kWave] * f1;
+      st.l = st.l * f0 + l1 * f1;
+      st.r = st.r * (f0 * f0) + xchg[(16 * kDB + 2) * kWave] * (f1 * f1);
+    }
+    return xchg;
+  };
+
+  prologue();
   // ---- pipelined main loop ---------------------------------------------------
   // Step k: MFMAs QK(k+1) [K_{k+1}, read at step k-1] and PV(k-1) [P_{k-1},
   // V_{k-1}] interleave with the softmax of S_k. S, P and the K fragments
@@ -634,53 +726,36 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     }
   }
 
-  // ---- short-row blocks: one plain split-P step per tile ---------------------
-  // Tile kk is resident (waited for by an earlier advance, or by the
-  // prologue); its fragments are read before the barrier that lets the load
-  // of tile kk + 4 overwrite its K stage.
-  for (; kk < n_steps; ++kk) {
-    const int key0 = ring.tile(kk) * kBc;
-    const bool active = key0 < wave_key_end;
-    KFrags<D> kf;
-    VFrags<D> vf;
-    if (active) {
-      read_k(ring.kstage(kk), fo, kf);
-      read_v(ring.vstage(kk), fo, vf);
+  split_steps(kk);
+  float *xchg = merge_halves();
+  if (!short_rows) {
+    // Every row of a half-0 wave now holds its final (l, r). One fp16
+    // rounding of each weight perturbs the output row by about 2^-11 times
+    // the root of the squared normalised weights that took it, r / l^2: a row
+    // that a few keys carry (beyond its exact P = 1 key) has a large r / l^2.
+    // Blocks with such a row run again with split P. Each half-0 wave leaves
+    // its verdict in its own (already consumed) exchange slot; after the
+    // barrier every wave reads all four.
+    if (half == 0) {
+      const float l_row = st.l + __shfl_xor(st.l, 32);
+      const float r_row = st.r + __shfl_xor(st.r, 32);
+      const bool peaky = my_q < seq && r_row > kRedoRoundedMassAbove * l_row * l_row;
+      const float verdict = __builtin_amdgcn_ballot_w64(peaky) != 0 ? 1.0f : 0.0f;
+      if (lane == 0) xchg[0] = verdict;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done
-    ring.advance(kk);
-    if (active) slow_step<CAUSAL, D>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
-  }
-
-  // ---- merge the two halves through LDS, normalise, store ------------------
-  // Layout: [row wave][34 values][64 lanes] fp32 from the start of LDS. Every
-  // load the ring issued has completed; the barrier ends every read of it.
-  wait_loads<0>();
-  __builtin_amdgcn_s_barrier();
-  float *xchg = reinterpret_cast<float *>(lds) + rw * (G::kXchg * kWave) + lane;
-  if (half == 1) {
+    __syncthreads();
+    bool redo = false;
 #pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) xchg[(16 * db + a) * kWave] = st.o[db][a];
-    xchg[16 * kDB * kWave] = st.m;
-    xchg[(16 * kDB + 1) * kWave] = st.l;
+    for (int r = 0; r < kRowWaves; ++r)
+      redo = redo || reinterpret_cast<const float *>(lds)[r * (G::kXchg * kWave)] != 0.0f;
+    if (redo) {
+      __syncthreads();  // every wave has read the verdicts before the LDS is reloaded
+      prologue();
+      split_steps(0);
+      merge_halves();
+    }
   }
-  __syncthreads();
   if (half == 1) return;
-  {
-    const float m1 = xchg[16 * kDB * kWave];
-    const float l1 = xchg[(16 * kDB + 1) * kWave];
-    const float m = fmaxf(st.m, m1);
-    const float f0 = fast_exp2(st.m - m);
-    const float f1 = fast_exp2(m1 - m);
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int a = 0; a < 16; ++a)
-        st.o[db][a] = st.o[db][a] * f0 + xchg[(16 * db + a) * kWave] * f1;
-    st.l = st.l * f0 + l1 * f1;
-  }
 
   // ---- epilogue: O = O^T / l, one query row per lane -------------------------
   const int g = lane >> 5;
@@ -754,10 +829,11 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
   const int group = heads / kv_heads;
   const float c_scale = fabsf(scale) * kLog2e;
   const bool negate_q = scale < 0.f;
-  // Logits much wider than N(0,1) at 1/sqrt(D) make rows peaky at any length,
-  // where one fp16 rounding of P costs up to ~5e-4 (measured: D = 128 at
-  // scale 0.3, 3.4x the standard width): every row then takes the split-P
-  // step.
+  // A scale well above 1/sqrt(D) makes rows peaky at any length (one fp16
+  // rounding of P costs up to ~5e-4 at D = 128, scale 0.3): the single-
+  // rounding pass would be redone for nearly every block, so every row takes
+  // the split-P step from the start. Wide inputs at a standard scale are
+  // caught per block by the rounded-mass check in the kernel.
   const bool split_all = fabsf(scale) * sqrtf(static_cast<float>(head_dim)) > kSplitAllWidth;
   if (head_dim == 128)
     launch_d<128>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, split_all,
