@@ -94,6 +94,8 @@
 // N(0,1) inputs at 1/sqrt(D) stay below 0.065 (rows with 256-383 keys) and
 // below 0.045 beyond, so they take the single-rounding pass only.
 
+#include <type_traits>
+
 #include "fa_internal.h"
 #include "mfma_tile.h"
 
@@ -142,9 +144,18 @@ struct Geo {
   static constexpr int kQHalves = kQInLds ? kBr * D : 0;                  // 16 KiB / 0
   static constexpr int kHalfHalves = (kKStages + kVStages) * kTileHalves; // 72 KiB
   static constexpr int kLdsHalves = kQHalves + 2 * kHalfHalves;           // 160 / 144 KiB
-  // Half-merge exchange at the end: [row wave][O^T values, m, l, r][64 lanes] fp32.
-  static constexpr int kXchg = 16 * kDB + 3;
-  static_assert(kRowWaves * kXchg * kWave * 4 <= kLdsHalves * 2, "exchange fits in LDS");
+  // Half-merge exchange at the end: [row wave][group][64 lanes][4] fp32, the
+  // groups holding the O^T values, then (m, l, r, unused); 16 B per lane and
+  // group, so each group is one conflict-free ds_write_b128 / ds_read_b128.
+  static constexpr int kXchg = 16 * kDB + 4;  // floats per lane
+  static constexpr int kXchgBytes = kRowWaves * kXchg * kWave * 4;
+  // Output staging after the exchange: per row wave, its 32 rows of O,
+  // row-major with 16-byte chunks XOR-swizzled by row, so that each lane can
+  // store 16 contiguous bytes and a store instruction covers whole rows.
+  template <bool F32>
+  static constexpr int kOutRowBytes = D * (F32 ? 4 : 2);
+  static_assert(kXchgBytes + kRowWaves * kRowsPerWave * kOutRowBytes<true> <= kLdsHalves * 2,
+                "exchange and output staging fit in LDS");
 };
 
 
@@ -599,37 +610,39 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     }
   };
   auto merge_halves = [&]() -> float * {
-    // ---- merge the two halves through LDS, normalise, store ------------------
-    // Layout: [row wave][kXchg values][64 lanes] fp32 from the start of LDS. Every
-    // load the ring issued has completed; the barrier ends every read of it.
+    // ---- merge the two halves through LDS ---------------------------------------
+    // Every load the ring issued has completed; the barrier ends every read of it.
     wait_loads<0>();
     __builtin_amdgcn_s_barrier();
-    float *xchg = reinterpret_cast<float *>(lds) + rw * (G::kXchg * kWave) + lane;
+    float *xbase = reinterpret_cast<float *>(lds) + rw * (G::kXchg * kWave);
+    floatx4 *xg = reinterpret_cast<floatx4 *>(xbase) + lane;  // group i at xg[i * kWave]
     if (half == 1) {
 #pragma unroll
       for (int db = 0; db < kDB; ++db)
 #pragma unroll
-        for (int a = 0; a < 16; ++a) xchg[(16 * db + a) * kWave] = st.o[db][a];
-      xchg[16 * kDB * kWave] = st.m;
-      xchg[(16 * kDB + 1) * kWave] = st.l;
-      xchg[(16 * kDB + 2) * kWave] = st.r;
+        for (int i = 0; i < 4; ++i)
+          xg[(4 * db + i) * kWave] = {st.o[db][4 * i], st.o[db][4 * i + 1], st.o[db][4 * i + 2],
+                                      st.o[db][4 * i + 3]};
+      xg[4 * kDB * kWave] = {st.m, st.l, st.r, 0.f};
     }
     __syncthreads();
     if (half == 0) {
-      const float m1 = xchg[16 * kDB * kWave];
-      const float l1 = xchg[(16 * kDB + 1) * kWave];
-      const float m = fmaxf(st.m, m1);
+      const floatx4 mlr = xg[4 * kDB * kWave];
+      const float m = fmaxf(st.m, mlr[0]);
       const float f0 = fast_exp2(st.m - m);
-      const float f1 = fast_exp2(m1 - m);
+      const float f1 = fast_exp2(mlr[0] - m);
 #pragma unroll
       for (int db = 0; db < kDB; ++db)
 #pragma unroll
-        for (int a = 0; a < 16; ++a)
-          st.o[db][a] = st.o[db][a] * f0 + xchg[(16 * db + a) * kWave] * f1;
-      st.l = st.l * f0 + l1 * f1;
-      st.r = st.r * (f0 * f0) + xchg[(16 * kDB + 2) * kWave] * (f1 * f1);
+        for (int i = 0; i < 4; ++i) {
+          const floatx4 o1 = xg[(4 * db + i) * kWave];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st.o[db][4 * i + e] = st.o[db][4 * i + e] * f0 + o1[e] * f1;
+        }
+      st.l = st.l * f0 + mlr[1] * f1;
+      st.r = st.r * (f0 * f0) + mlr[2] * (f1 * f1);
     }
-    return xchg;
+    return xbase;
   };
 
   prologue();
@@ -757,30 +770,53 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }
   if (half == 1) return;
 
-  // ---- epilogue: O = O^T / l, one query row per lane -------------------------
-  const int g = lane >> 5;
-  const float l_tot = st.l + __shfl_xor(st.l, 32);
-  const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-  if (my_q < seq) {
-    const size_t row_off = head_off + static_cast<size_t>(my_q) * D;
+  // ---- epilogue: O = O^T / l --------------------------------------------------
+  // Each lane holds one query row; it writes its row's values to this row
+  // wave's staging area, then the wave stores whole rows: lane i of a store
+  // instruction takes 16-byte chunk i % kChunksOut of row i / kChunksOut.
+  {
+    using OutT = typename std::conditional<OUT_F32, float, _Float16>::type;
+    constexpr int kRowBytes = G::template kOutRowBytes<OUT_F32>;
+    constexpr int kChunksOut = kRowBytes / 16;          // 16-byte chunks per row
+    constexpr int kRowsPerStore = kWave / kChunksOut;    // rows per store instruction
+    const int g = lane >> 5;
+    const float l_tot = st.l + __shfl_xor(st.l, 32);
+    const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+    char *stage = reinterpret_cast<char *>(lds) + G::kXchgBytes +
+                  rw * (kRowsPerWave * kRowBytes);
+    const int swz = col & (kChunksOut - 1);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int d = db * 32 + 8 * jj + 4 * g;  // 4 consecutive dims
-        if (OUT_F32) {
+        // dims [32 db + 8 jj + 4 g, +4)
+        if constexpr (OUT_F32) {
           floatx4 r;
 #pragma unroll
           for (int e = 0; e < 4; ++e) r[e] = st.o[db][4 * jj + e] * inv_l;
-          *reinterpret_cast<floatx4 *>(static_cast<float *>(o) + row_off + d) = r;
+          const int chunk = 8 * db + 2 * jj + g;
+          *reinterpret_cast<floatx4 *>(stage + col * kRowBytes + 16 * (chunk ^ swz)) = r;
         } else {
           half4 r;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            r[e] = static_cast<_Float16>(st.o[db][4 * jj + e] * inv_l);
-          *reinterpret_cast<half4 *>(static_cast<_Float16 *>(o) + row_off + d) = r;
+          for (int e = 0; e < 4; ++e) r[e] = static_cast<_Float16>(st.o[db][4 * jj + e] * inv_l);
+          const int chunk = 4 * db + jj;
+          *reinterpret_cast<half4 *>(stage + col * kRowBytes + 16 * (chunk ^ swz) + 8 * g) = r;
         }
       }
+    }
+    // The wave reads back only what it wrote itself: its LDS operations
+    // complete in order, so no barrier is needed.
+    const int chunk = lane % kChunksOut;
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / kRowsPerStore; ++i) {
+      const int r = i * kRowsPerStore + lane / kChunksOut;
+      const floatx4 val =
+          *reinterpret_cast<const floatx4 *>(stage + r * kRowBytes + 16 * (chunk ^ (r & (kChunksOut - 1))));
+      if (qw0 + r < seq)
+        *reinterpret_cast<floatx4 *>(reinterpret_cast<char *>(static_cast<OutT *>(o) + head_off +
+                                                               static_cast<size_t>(qw0 + r) * D) +
+                                     16 * chunk) = val;
     }
   }
 }
