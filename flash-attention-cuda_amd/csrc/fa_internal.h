@@ -15,6 +15,8 @@ namespace fa {
 
 constexpr int kHeadDim = FA_HEAD_DIM;
 constexpr int kMaxDevices = 64;  // per-device host caches
+// Split-K scratch that fa_decode_hd_noalloc keeps per device (8 MiB).
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 

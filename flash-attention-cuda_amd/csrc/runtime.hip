@@ -15,7 +15,17 @@
 
 #include "fa_internal.h"
 
+// Split-K partials of fa_decode_hd_noalloc: one copy of this array per
+// device, part of the library's code object, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host it names
+// a stand-in, not device memory); it uses the address that
+// hipGetSymbolAddress returns for the current device (device_scratch below).
+static __device__ __align__(256) float scratch[fa::kNoAllocScratchBytes / sizeof(float)];
+
 namespace fa {
+
+static_assert(kNoAllocScratchBytes == FA_NOALLOC_SCRATCH_BYTES,
+              "scratch size and its public constant agree");
 
 namespace {
 thread_local char g_last_error[512] = "";
@@ -27,6 +37,32 @@ int g_cu_count[kMaxDevices];
 
 bool aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+std::once_flag g_scratch_once[kMaxDevices];
+void *g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int device_scratch(void **ptr) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != FA_OK) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(FA_ERR_HIP, "device %d is beyond the %d devices the library tracks", dev,
+                     kMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void *p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  rc = check_hip(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+  if (rc != FA_OK) return rc;
+  if (g_scratch_ptr[dev] == nullptr)
+    return set_error(FA_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+  *ptr = g_scratch_ptr[dev];
+  return FA_OK;
 }
 }  // namespace
 
@@ -224,10 +260,13 @@ size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq, in
   return decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
 }
 
+// scratch_ws: the workspace is the library's own per-device scratch
+// (fa_decode_hd_noalloc), which only changes the message of a size failure.
 int decode_impl(const void *q, const void *k_cache, const void *v_cache,
                 const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
                 int kv_heads, int max_seq, int head_dim, float scale, int split_size,
-                void *workspace, size_t workspace_bytes, void *stream) {
+                void *workspace, size_t workspace_bytes, void *stream,
+                bool scratch_ws = false) {
   clear_error();
   if (check_head_dim(head_dim) != FA_OK) return FA_ERR_INVALID_ARGUMENT;
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
@@ -259,6 +298,11 @@ int decode_impl(const void *q, const void *k_cache, const void *v_cache,
   if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
     return set_error(FA_ERR_INVALID_ARGUMENT, "too many split blocks");
   const size_t need = decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
+  if (scratch_ws && need > workspace_bytes)
+    return set_error(FA_ERR_WORKSPACE,
+                     "fa_decode_hd_noalloc: this shape needs %zu bytes of split-K scratch, "
+                     "above the library's fixed %zu bytes; call fa_decode_hd with a workspace",
+                     need, workspace_bytes);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(FA_ERR_WORKSPACE,
                      "decode workspace too small: need %zu bytes, got %zu", need,
@@ -337,6 +381,21 @@ int fa_decode_hd(const void *q, const void *k_cache, const void *v_cache,
                  void *workspace, size_t workspace_bytes, void *stream) {
   return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, kv_heads,
                      max_seq, head_dim, scale, split_size, workspace, workspace_bytes, stream);
+}
+
+// No reference counterpart: fa_decode_hd for callers that cannot allocate.
+// Its split-K partials go to the library's per-device scratch array.
+int fa_decode_hd_noalloc(const void *q, const void *k_cache, const void *v_cache,
+                         const int32_t *seq_lens, void *o, int out_dtype, int batch, int heads,
+                         int kv_heads, int max_seq, int head_dim, float scale, int split_size,
+                         void *stream) {
+  clear_error();
+  void *ws = nullptr;
+  const int rc = device_scratch(&ws);
+  if (rc != FA_OK) return rc;
+  return decode_impl(q, k_cache, v_cache, seq_lens, o, out_dtype, batch, heads, kv_heads,
+                     max_seq, head_dim, scale, split_size, ws, kNoAllocScratchBytes, stream,
+                     true);
 }
 
 namespace {

@@ -38,6 +38,8 @@
  *                               work in the reference (README.md:230, :397);
  *                               with head_dim 64 they are fa_prefill_gqa /
  *                               fa_decode_gqa / fa_kv_append.
+ *   fa_decode_hd_noalloc     <- no counterpart: fa_decode_hd without a workspace
+ *                               argument, for callers that cannot allocate.
  *   fa_legacy_attention      <- launch_naive_attention / launch_tiled_attention /
  *                               launch_fused_attention,
  *                               src/legacy/{naive,tiled,fused}_attention.cu
@@ -192,6 +194,25 @@ int fa_decode_hd(const void *q, const void *k_cache, const void *v_cache,
 int fa_kv_append_hd(void *k_cache, void *v_cache, const void *k_new,
                     const void *v_new, int32_t *seq_lens, int batch,
                     int kv_heads, int max_seq, int head_dim, void *stream);
+
+/* No counterpart in the reference: fa_decode_hd for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * hosts that forbid allocation). It takes no workspace and calls no
+ * hipMalloc / hipFree: the split-K partials go to a scratch array of
+ * FA_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
+ * until the process ends. A shape whose partials need more fails with
+ * FA_ERR_WORKSPACE before anything is launched (fa_decode_hd_workspace_bytes
+ * gives the need). Every call on one device shares that device's array and
+ * leaves its contents behind: calls that overlap in time on one device
+ * (several streams or threads) race, so the caller must serialise them.
+ * Same arguments, rules and results as fa_decode_hd otherwise. */
+#define FA_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+int fa_decode_hd_noalloc(const void *q, const void *k_cache,
+                         const void *v_cache, const int32_t *seq_lens, void *o,
+                         int out_dtype, int batch, int heads, int kv_heads,
+                         int max_seq, int head_dim, float scale, int split_size,
+                         void *stream);
 
 /* The reference's v1 single-head kernels: o = softmax(q k^T / sqrt(64)) v
  * for q, k, v, o of shape (n, 64) fp32, row-major, no mask. The three

@@ -53,6 +53,7 @@ def test_header_declares_the_expected_entry_points():
             "fa_decode_gqa",
             "fa_decode_gqa_workspace_bytes",
             "fa_decode_hd",
+            "fa_decode_hd_noalloc",
             "fa_decode_hd_workspace_bytes",
             "fa_decode_min_blocks",
             "fa_decode_workspace_bytes",
