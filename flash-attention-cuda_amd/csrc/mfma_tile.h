@@ -56,6 +56,20 @@ __device__ __forceinline__ void global_to_lds16(const void *src, const void *lds
       : "v"(src), "s"(m0)
       : "memory", "m0");
 }
+// The same load with a wave-uniform 64-bit base in SGPRs and a per-lane
+// 32-bit byte offset (the saddr form): no per-lane address arithmetic.
+__device__ __forceinline__ void global_to_lds16_sbase(const void *base, unsigned voff,
+                                                      const void *lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(lds_dst))));
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Wait until at most N of this thread's global->LDS loads are outstanding.
@@ -153,6 +167,21 @@ typedef __attribute__((address_space(3))) const _Float16 lds_half;
 // separate loop-invariant addresses.
 __device__ __forceinline__ lds_half *opaque_lds(const _Float16 *p) {
   unsigned a = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p)));
+  asm volatile("" : "+v"(a));
+  return reinterpret_cast<lds_half *>(static_cast<uintptr_t>(a));
+}
+
+// LDS address base + 2 * off_halves, with base a wave-uniform tile address
+// kept whole in an SGPR (so no constant part of it is split off into a
+// separate vector add) and the sum opaque as in opaque_lds.
+__device__ __forceinline__ unsigned uniform_lds_base(const _Float16 *p) {
+  unsigned a = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p))));
+  asm volatile("" : "+s"(a));
+  return a;
+}
+__device__ __forceinline__ lds_half *opaque_lds_at(unsigned base, int off_halves) {
+  unsigned a = base + 2u * static_cast<unsigned>(off_halves);
   asm volatile("" : "+v"(a));
   return reinterpret_cast<lds_half *>(static_cast<uintptr_t>(a));
 }

@@ -94,6 +94,7 @@
 // N(0,1) inputs at 1/sqrt(D) stay below 0.065 (rows with 256-383 keys) and
 // below 0.045 beyond, so they take the single-rounding pass only.
 
+#include <algorithm>
 #include <type_traits>
 
 #include "fa_internal.h"
@@ -182,9 +183,10 @@ struct VFrags { half8 f[Geo<D>::kKS][Geo<D>::kDB]; };  // [16-key step][d-block]
 template <int D>
 __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
                                        const FragOffsetsD<D> &fo, KFrags<D> &k) {
+  const unsigned base = uniform_lds_base(tile);
 #pragma unroll
   for (int s = 0; s < Geo<D>::kDS; ++s) {
-    lds_half *p = opaque_lds(tile + fo.k[s]);
+    lds_half *p = opaque_lds_at(base, fo.k[s]);
 #pragma unroll
     for (int kb = 0; kb < Geo<D>::kKB; ++kb)
       k.f[kb][s] = *reinterpret_cast<__attribute__((address_space(3))) const half8 *>(
@@ -195,9 +197,10 @@ __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
 template <int D>
 __device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
                                        const FragOffsetsD<D> &fo, VFrags<D> &v) {
+  const unsigned base = uniform_lds_base(tile);
 #pragma unroll
   for (int db = 0; db < Geo<D>::kDB; ++db) {
-    lds_half *p = opaque_lds(tile + fo.v[db]);
+    lds_half *p = opaque_lds_at(base, fo.v[db]);
 #pragma unroll
     for (int ks = 0; ks < Geo<D>::kKS; ++ks) {
       const int kb = ks >> 1, h = ks & 1;
@@ -372,9 +375,9 @@ struct HalfRing {
   _Float16 *kring, *vring;
   const _Float16 *kp, *vp;
   int seq, n_tiles, half;
-  int src_off[2][2];  // [K|V][row block i]: this lane's chunk within its row
+  unsigned voff[2][2];  // [K|V][row block i]: byte offset of this lane's chunk in a tile
   int row_in_tile[2];
-  int lds_off[2];     // row block i of this wave, in halves
+  int lds_off[2];       // row block i of this wave, in halves
 
   __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
   __device__ __forceinline__ bool exists(int k) const { return tile(k) < n_tiles; }
@@ -394,11 +397,24 @@ struct HalfRing {
     const int key0 = tile(k) * G::kBc;
     _Float16 *const ks = kstage(k);
     _Float16 *const vs = vstage(k);
+    if (key0 + G::kBc <= seq) {
+      // Whole tile inside the sequence: a scalar tile base plus the lane's
+      // fixed offset.
+      const _Float16 *const kb = kp + static_cast<size_t>(key0) * D;
+      const _Float16 *const vb = vp + static_cast<size_t>(key0) * D;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * D;
-      global_to_lds16(kp + row + src_off[0][i], ks + lds_off[i]);
-      global_to_lds16(vp + row + src_off[1][i], vs + lds_off[i]);
+      for (int i = 0; i < 2; ++i) {
+        global_to_lds16_sbase(kb, voff[0][i], ks + lds_off[i]);
+        global_to_lds16_sbase(vb, voff[1][i], vs + lds_off[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int in_row = row_in_tile[i] * D;
+        const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * D;
+        global_to_lds16(kp + row + (voff[0][i] / 2 - in_row), ks + lds_off[i]);
+        global_to_lds16(vp + row + (voff[1][i] / 2 - in_row), vs + lds_off[i]);
+      }
     }
   }
   // Start of main step k: this half's tiles up to k + 2 are resident and
@@ -470,7 +486,7 @@ template <int D, bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
-    int n_qtiles, int group, float c_scale, bool negate_q, bool split_all) {
+    int n_qtiles, int bh_count, int group, float c_scale, bool negate_q, bool split_all) {
   using G = Geo<D>;
   constexpr int kBc = G::kBc;
   constexpr int kKB = G::kKB;
@@ -479,13 +495,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   constexpr int kDS = G::kDS;
   __shared__ __attribute__((aligned(1024))) _Float16 lds[G::kLdsHalves];
 
-  // Heaviest (last) query tiles first: one block fills a CU, so dispatching
-  // in decreasing work order is a longest-first list schedule.
-  const int bh_count = static_cast<int>(gridDim.x) / n_qtiles;
-  const int qtile = n_qtiles - 1 - static_cast<int>(blockIdx.x) / bh_count;
-  int bh = home_head(static_cast<int>(blockIdx.x), bh_count);
-  if (group > 1) bh = grouped_head(bh, bh_count);
-
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // Wave-uniform (SGPR) so every stage / row-block address below is scalar.
@@ -493,6 +502,47 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int rw = wave & (kRowWaves - 1);  // row wave: rows [32 rw, +32)
   const int half = wave / kRowWaves;      // key half: tiles 2k + half
   const int col = lane & 31;
+  _Float16 *const half_lds = lds + G::kQHalves + half * G::kHalfHalves;
+  _Float16 *const q_lds = lds;
+  HalfRing<D> ring;
+  ring.kring = half_lds;
+  ring.vring = half_lds + kKStages * G::kTileHalves;
+  ring.seq = seq;
+  ring.half = half;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rblock = 2 * rw + i;
+    const int r = rblock * G::kRowsPerLoad + lane / G::kChunks;
+    const int p = lane % G::kChunks;
+    ring.row_in_tile[i] = r;
+    ring.voff[0][i] = 2u * static_cast<unsigned>(r * D + ((p ^ k_swz_d<D>(r)) << 3));
+    ring.voff[1][i] = 2u * static_cast<unsigned>(r * D + ((p ^ v_swz_d<D>(r)) << 3));
+    ring.lds_off[i] = rblock * G::kRowsPerLoad * D;
+  }
+  const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
+
+  // Items are (b, h, 128-row query tile), numbered heaviest (last) query
+  // tile first. Block b of the G-block grid (G >= items / 2) takes item b,
+  // then item G + mirror(b) if there is one, so a block with a heavy first
+  // item gets a light second one: with causal masking, items b and ~2G - b
+  // sum to about the same work. The mirror reverses groups of 8 positions
+  // and keeps the position mod 8, the XCD the block runs on (blocks go to
+  // the 8 XCDs round-robin), which home_head uses for L2 placement. (Two
+  // unrolled rounds, no loop back-edge: the body keeps its registers.)
+  const int n_items = bh_count * n_qtiles;
+  const int grid = static_cast<int>(gridDim.x);
+  const int b_id = static_cast<int>(blockIdx.x);
+  const int b_mirror = (grid & 7) == 0 ? grid - 8 * (b_id / 8 + 1) + (b_id & 7) : grid - 1 - b_id;
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+  const int pos = round == 0 ? b_id : grid + b_mirror;
+  if (pos >= n_items) break;
+  // The previous item's last LDS accesses (output staging) end before this
+  // item's loads overwrite the LDS.
+  if (round > 0) __syncthreads();
+  const int qtile = n_qtiles - 1 - pos / bh_count;
+  int bh = home_head(pos, bh_count);
+  if (group > 1) bh = grouped_head(bh, bh_count);
 
   // Q and O are [B, H, S, 64], K and V [B, H / group, S, 64]: query head
   // b * H + h reads K/V head b * H / group + h / group = bh / group.
@@ -504,26 +554,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
   const int key_end = CAUSAL ? min(seq, q0 + kBr) : seq;
   const int n_tiles = (key_end + kBc - 1) / kBc;
-  _Float16 *const half_lds = lds + G::kQHalves + half * G::kHalfHalves;
-  _Float16 *const q_lds = lds;
-  HalfRing<D> ring;
-  ring.kring = half_lds;
-  ring.vring = half_lds + kKStages * G::kTileHalves;
   ring.kp = k + kv_off;
   ring.vp = v + kv_off;
-  ring.seq = seq;
   ring.n_tiles = n_tiles;
-  ring.half = half;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rblock = 2 * rw + i;
-    const int r = rblock * G::kRowsPerLoad + lane / G::kChunks;
-    const int p = lane % G::kChunks;
-    ring.row_in_tile[i] = r;
-    ring.src_off[0][i] = (p ^ k_swz_d<D>(r)) << 3;
-    ring.src_off[1][i] = (p ^ v_swz_d<D>(r)) << 3;
-    ring.lds_off[i] = rblock * G::kRowsPerLoad * D;
-  }
   const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
   // Tiles [0, 2 n_main) need no mask for any row of the block, and all its
   // rows see >= kSplitPRowsBelow keys: each half runs n_main pipelined steps
@@ -539,7 +572,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
 
-  const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
   half8 qf[kDS];
   SoftmaxState<D> st;
   auto prologue = [&]() {
@@ -768,7 +800,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       merge_halves();
     }
   }
-  if (half == 1) return;
+  if (half == 1) continue;
 
   // ---- epilogue: O = O^T / l --------------------------------------------------
   // Each lane holds one query row; it writes its row's values to this row
@@ -819,6 +851,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
                                      16 * chunk) = val;
     }
   }
+  }  // items
 }
 
 template <int D, bool CAUSAL, bool OUT_F32>
@@ -826,12 +859,19 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
                 int seq, int group, float c_scale, bool negate_q, bool split_all,
                 hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
-  const unsigned blocks = static_cast<unsigned>(bh) * n_qtiles;
+  const long long items = static_cast<long long>(bh) * n_qtiles;
+  // A block takes a whole CU's LDS and up to two items: one block per CU,
+  // or half the items when there are more than two per CU; without a CU
+  // count, one block per item.
+  int dev = 0;
+  const int cu = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
+  const unsigned blocks = static_cast<unsigned>(
+      cu > 0 ? std::min<long long>(items, std::max<long long>(cu, (items + 1) / 2)) : items);
   hipLaunchKernelGGL((prefill_kernel<D, CAUSAL, OUT_F32>), dim3(blocks),
                      dim3(kThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
-                     static_cast<const _Float16 *>(v), o, seq, n_qtiles, group,
+                     static_cast<const _Float16 *>(v), o, seq, n_qtiles, bh, group,
                      c_scale, negate_q, split_all);
 }
 
