@@ -191,17 +191,21 @@ at::Tensor decode_core(const at::Tensor &q, const at::Tensor &k_cache,
   const int head_dim = static_cast<int>(q.size(3));
   const size_t ws_bytes =
       fa_decode_hd_workspace_bytes(batch, heads, kv_heads, max_seq, head_dim, split);
-  check_status(ws_bytes > 0 ? FA_OK : FA_ERR_INVALID_ARGUMENT);
+  // 0 bytes: the whole-sequence kernel needs no workspace, unless the query
+  // failed (then fa_last_error() says why).
+  check_status(ws_bytes > 0 || fa_last_error()[0] == '\0' ? FA_OK : FA_ERR_INVALID_ARGUMENT);
   // Transient, stream-ordered workspace from the caching allocator
-  // (decode.cu:215-219 of the reference).
-  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes / sizeof(float))},
-                            q.options().dtype(at::kFloat));
+  // (decode.cu:215-219 of the reference), only when the split-K partials need it.
+  at::Tensor ws;
+  if (ws_bytes > 0)
+    ws = at::empty({static_cast<int64_t>(ws_bytes / sizeof(float))},
+                   q.options().dtype(at::kFloat));
   check_status(fa_decode_hd(q.const_data_ptr(), k_cache.const_data_ptr(),
                             v_cache.const_data_ptr(),
                             seq_lens.const_data_ptr<int32_t>(), o.data_ptr(),
                             out_f32 ? FA_OUT_F32 : FA_OUT_F16, batch, heads, kv_heads,
                             max_seq, head_dim, static_cast<float>(scale), split,
-                            ws.data_ptr(), ws_bytes, stream_of(q)));
+                            ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
   return o;
 }
 

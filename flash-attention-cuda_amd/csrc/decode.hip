@@ -687,9 +687,19 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  int b = static_cast<int>(blockIdx.x) / heads;
-  const int h = static_cast<int>(blockIdx.x) % heads;
-  if (batch <= kRankMax) {
+  // Block -> position in the longest-first order. With the whole grid
+  // resident (target_waves = kBhWavesPerCu x CUs), blocks [0, CUs) take one
+  // CU each and block CUs + j lands on the CU of block j: the second round
+  // takes the positions in reverse, so a CU pairs a long sequence with a
+  // short one.
+  int pos = static_cast<int>(blockIdx.x);
+  const int n_blocks = static_cast<int>(gridDim.x);
+  const int cus = target_waves / kBhWavesPerCu;
+  if (target_waves > 0 && pos >= cus) pos = cus + (n_blocks - 1 - pos);
+  int b = pos / heads;
+  const int h = pos % heads;
+  const bool ranked = batch <= kRankMax;
+  if (ranked) {
     // rank(t) = #{u : len_u > len_t or (len_u == len_t and u < t)}: block i
     // takes the (i / H)-th longest sequence.
     for (int t = tid; t < batch; t += kBhThreads) s_len[t] = max(0, min(seq_lens[t], max_seq));
@@ -707,19 +717,27 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
     b = s_order[b];
   }
   const int bh = b * heads + h;
+  const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
+  const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
+  // The query is loaded here, with the lengths, so both loads are in flight
+  // together.
+  half2 qh[4];
+  load_query<D>(q, bh, slice, qh);
   const int len = max(0, min(seq_lens[b], max_seq));
   if (chunk == 0) {
     int rows_per_wave;
     if (target_waves > 0) {
       int part = 0;
-      for (int t = lane; t < batch; t += kWave)
-        part += batch <= kRankMax ? s_len[t] : max(0, min(seq_lens[t], max_seq));
+      for (int t = lane; t < batch; t += kWave) part += max(0, min(seq_lens[t], max_seq));
 #pragma unroll
       for (int off = kWave / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
       const float total = static_cast<float>(__builtin_amdgcn_readfirstlane(part));
       rows_per_wave = static_cast<int>(
           fminf(ceilf(total * static_cast<float>(heads) / static_cast<float>(target_waves)),
                 static_cast<float>(max_seq)));
+      // No wave takes a second chunk: that would double its time, and the
+      // whole block waits for it.
+      rows_per_wave = max(rows_per_wave, (len + kBhWaves - 1) / kBhWaves);
     } else {
       rows_per_wave = (len + kBhWaves - 1) / kBhWaves;
     }
@@ -727,8 +745,6 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   }
   chunk = min(chunk, max_seq);  // max_seq <= 2^27 (host check): 8 * chunk fits in int
 
-  const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
-  const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
   const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
   const _Float16 *kp = k_cache + head_off;
   const _Float16 *vp = v_cache + head_off;
@@ -741,8 +757,6 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   const int stride = kBhWaves * chunk;  // distance between a wave's chunks
   int c0 = wave * chunk;                // this wave's current chunk
   if (c0 < len) {
-    half2 qh[4];
-    load_query<D>(q, bh, slice, qh);
     int end = min(len, c0 + chunk);
     int row0 = c0;
     RowSlotsT<kBhGroups> cur, nxt;
@@ -853,6 +867,10 @@ int group_queries(int group) {
 
 
 }  // namespace
+
+bool decode_needs_workspace(int batch, int heads, int kv_heads, int max_seq) {
+  return heads != kv_heads || !use_bh_path(batch, heads, max_seq);
+}
 
 int decode_units_per_row(int heads, int kv_heads) {
   const int group = heads / kv_heads;

@@ -49,6 +49,10 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
                   const int32_t *seq_lens, void *o, bool out_f32, int batch,
                   int heads, int kv_heads, int max_seq, int head_dim, float scale,
                   int split_size, bool auto_split, float *workspace, hipStream_t stream);
+// Whether launch_decode writes split-K partials to its workspace for this
+// shape on the current device: the whole-sequence kernel (no grouped queries,
+// B * H >= CUs or a short cache) merges in LDS and needs none.
+bool decode_needs_workspace(int batch, int heads, int kv_heads, int max_seq);
 // Decode work units per batch row: one per head without grouped queries,
 // else one per (K/V head, chunk of up to 32 of its query heads).
 int decode_units_per_row(int heads, int kv_heads);

@@ -257,6 +257,7 @@ size_t decode_workspace_impl(int batch, int heads, int kv_heads, int max_seq, in
   if (check_head_dim(head_dim) != FA_OK) return 0;
   if (check_groups(heads, kv_heads) != FA_OK) return 0;
   if (resolve_split(batch, heads, kv_heads, max_seq, head_dim, &split_size) != FA_OK) return 0;
+  if (!decode_needs_workspace(batch, heads, kv_heads, max_seq)) return 0;
   return decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
 }
 
@@ -297,17 +298,19 @@ int decode_impl(const void *q, const void *k_cache, const void *v_cache,
   const size_t n_splits = (static_cast<size_t>(max_seq) + split_size - 1) / split_size;
   if (static_cast<size_t>(batch) * heads * n_splits > 0x7fffffffull)
     return set_error(FA_ERR_INVALID_ARGUMENT, "too many split blocks");
-  const size_t need = decode_ws_bytes(batch, heads, max_seq, head_dim, split_size);
+  const size_t need = decode_needs_workspace(batch, heads, kv_heads, max_seq)
+                          ? decode_ws_bytes(batch, heads, max_seq, head_dim, split_size)
+                          : 0;
   if (scratch_ws && need > workspace_bytes)
     return set_error(FA_ERR_WORKSPACE,
                      "fa_decode_hd_noalloc: this shape needs %zu bytes of split-K scratch, "
                      "above the library's fixed %zu bytes; call fa_decode_hd with a workspace",
                      need, workspace_bytes);
-  if (workspace == nullptr || workspace_bytes < need)
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return set_error(FA_ERR_WORKSPACE,
                      "decode workspace too small: need %zu bytes, got %zu", need,
                      workspace == nullptr ? size_t{0} : workspace_bytes);
-  if (!aligned16(workspace))
+  if (need > 0 && !aligned16(workspace))
     return set_error(FA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   return launch_decode(q, k_cache, v_cache, seq_lens, o, out_dtype == FA_OUT_F32,
                        batch, heads, kv_heads, max_seq, head_dim, scale, split_size, auto_split,

@@ -124,8 +124,11 @@ int fa_prefill(const void *q, const void *k, const void *v, void *o,
                void *stream);
 
 /* Bytes of device workspace fa_decode needs. split_size 0 selects the chunk
- * the same way fa_decode does (it queries the current device). Returns 0 and
- * sets fa_last_error() on invalid arguments. */
+ * the same way fa_decode does (it queries the current device). Returns 0
+ * with fa_last_error() empty when the call needs no workspace (the
+ * whole-sequence kernel, which merges in LDS: B * H at least the device's
+ * compute-unit count, or Lmax <= 512; fa_decode then accepts NULL), and 0
+ * with fa_last_error() set on invalid arguments. */
 size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,
                                  int split_size);
 

@@ -344,6 +344,33 @@ def test_decode_whole_sequence_path_matches_oracle(label, batch, heads, max_seq)
     assert not o[0].any() and not o[1].any()  # len 0 and len < 0: zero rows
 
 
+def test_decode_whole_sequence_path_takes_no_workspace():
+    """The whole-sequence kernel merges its waves in LDS: the C ABI reports 0
+    workspace bytes (with no error) for such a shape, accepts a NULL
+    workspace, and gives the same bits as the Python entry point."""
+    lib = ctypes.CDLL(LIB)
+    lib.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_last_error.restype = ctypes.c_char_p
+    batch, heads, max_seq = 32, 14, 700
+    assert lib.fa_decode_workspace_bytes(batch, heads, max_seq, 0) == 0
+    assert lib.fa_last_error() == b""
+    lens = _ragged_lens(batch, max_seq, seed=24)
+    q, k, v, lens = oracle.make_decode_inputs(batch, heads, max_seq, seed=25, lens=lens)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    o = torch.empty_like(qd)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.fa_decode(ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(kd.data_ptr()),
+                       ctypes.c_void_p(vd.data_ptr()), ctypes.c_void_p(ld.data_ptr()),
+                       ctypes.c_void_p(o.data_ptr()), 0, batch, heads, max_seq,
+                       ctypes.c_float(SCALE), 0, None, ctypes.c_size_t(0), stream)
+    assert rc == 0, lib.fa_last_error()
+    want = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o, want)
+    # The split-K shape still needs (and checks) its workspace.
+    assert lib.fa_decode_workspace_bytes(1, 12, 4096, 0) > 0
+
+
 def test_decode_whole_sequence_split_invariance_fp32():
     q, k, v, lens = oracle.make_decode_inputs(32, 10, 1500, seed=22,
                                               lens=_ragged_lens(32, 1500, seed=23))
