@@ -205,6 +205,100 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
   m = m_new;
 }
 
+// Single-launch merge: the wave that finishes a (b, h)'s last live group of
+// chunks merges all of its partials itself, so the split pass needs no
+// second kernel. It is found with one counter per (b, h): each group
+// publishes its partial, then counts itself; the wave that sees the count
+// reach the number of live groups merges and sets the counter back to zero,
+// so a finished call leaves every counter at zero. The counters are zero when
+// the code object loads and are split into slots, one per (device, stream)
+// in use, so calls that may overlap in time (other streams) never share one.
+constexpr int kCounterSlots = 64;
+constexpr int kCountersPerSlot = 4096;
+__device__ unsigned g_merge_counters[kCounterSlots * kCountersPerSlot];
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Partials that another wave of the same launch reads: relaxed agent-scope
+// atomic stores and loads, which go to the device-coherent level (sc1) on
+// their own, so the only ordering needed is the writer's wait for its stores
+// before it counts (no cache-wide release or acquire).
+__device__ __forceinline__ void store_coherent(float *p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave merges the n_act partials of one (b, h) (slots base .. base +
+// n_act - 1) with the log-sum-exp rule of the merge pass below and writes
+// the output row; lane j owns head dims j and j + 64.
+template <int D, bool OUT_F32>
+__device__ __forceinline__ void merge_partials_wave(const float *__restrict__ part_acc,
+                                                    const float *__restrict__ part_ml,
+                                                    size_t base, int n_act, void *o,
+                                                    size_t bh, int lane) {
+  constexpr int kDims = D / kWave;  // head dims per lane (1 or 2)
+  constexpr int kRound = 32;        // partial rows loaded in one round
+  // One round of loads for up to kRound chunks: every (m, l) and this lane's
+  // head dims of every partial row are issued before any is used.
+  float m_all = kNegBig, l_part = 0.f, ms = kNegBig, ls = 0.f;
+  float acc[kDims];
+#pragma unroll
+  for (int j = 0; j < kDims; ++j) acc[j] = 0.f;
+  for (int s0 = 0; s0 < n_act; s0 += kRound) {
+    const int cnt = min(kRound, n_act - s0);
+    const int sl = s0 + (lane & (kRound - 1));
+    const bool own = lane < kRound && sl < n_act;  // lane holds chunk sl's (m, l)
+    if (own) {
+      ms = load_coherent(part_ml + (base + sl) * 2);
+      ls = load_coherent(part_ml + (base + sl) * 2 + 1);
+    } else {
+      ms = kNegBig;
+      ls = 0.f;
+    }
+    float x[kRound][kDims];
+#pragma unroll
+    for (int u = 0; u < kRound; ++u)
+#pragma unroll
+      for (int j = 0; j < kDims; ++j)
+        x[u][j] = u < cnt ? load_coherent(part_acc + (base + s0 + u) * D + lane + kWave * j) : 0.f;
+    // Running log-sum-exp over the rounds (one round for <= kRound chunks).
+    const float m_new = fmaxf(m_all, wave_max(ms));
+    const float f = fast_exp2(m_all - m_new);
+    const float w = own ? fast_exp2(ms - m_new) : 0.f;
+    l_part = l_part * f + ls * w;
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) acc[j] *= f;
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) {
+      const float wu = __shfl(w, u);
+#pragma unroll
+      for (int j = 0; j < kDims; ++j) acc[j] = fmaf(x[u][j], wu, acc[j]);
+    }
+    m_all = m_new;
+  }
+  const float l_all = wave_sum(l_part);
+#pragma unroll
+  for (int j = 0; j < kDims; ++j) {
+    const float out = l_all > 0.f ? acc[j] / l_all : 0.f;
+    const size_t idx = bh * D + lane + kWave * j;
+    if (OUT_F32)
+      static_cast<float *>(o)[idx] = out;
+    else
+      static_cast<_Float16 *>(o)[idx] = static_cast<_Float16>(out);
+  }
+}
+
 // Pass 1 (decode.cu:50-138): one wave folds cache rows
 // [chunk_i * chunk, min(len, (chunk_i + 1) * chunk)) of one (b, h) into a
 // partial (m, l, acc[D]). Unit u = chunk_i * (B * H) + (b * H + h) is
@@ -286,6 +380,125 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
   }
 }
 
+// Single-launch split-K: a block of W waves takes W consecutive chunks
+// (group g) of one (b, h). The waves merge through LDS, wave 0 publishes the
+// group's partial and counts it, and the wave that counts the (b, h)'s last
+// live group merges the group partials and writes o. Grouping cuts the
+// partials, and the counter increments that contend on one (b, h), by W.
+template <int D, bool OUT_F32, int W>
+__global__ __launch_bounds__(W * kWave) void decode_split_fused_kernel(
+    const _Float16 *__restrict__ q, const _Float16 *__restrict__ k_cache,
+    const _Float16 *__restrict__ v_cache, const int32_t *__restrict__ seq_lens,
+    float *__restrict__ part_acc, float *__restrict__ part_ml, int heads, int max_seq,
+    int n_groups, int chunk, float qscale, unsigned *__restrict__ counters,
+    void *__restrict__ o) {
+  __shared__ float s_acc[W][D];
+  __shared__ float s_ml[W][2];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int bh = static_cast<int>(blockIdx.x) / n_groups;
+  const int g = static_cast<int>(blockIdx.x) % n_groups;
+  const int b = bh / heads;
+  const int len = min(seq_lens[b], max_seq);
+  if (len <= 0) {
+    // decode.cu:172: a sequence with no rows gets a zero output.
+    if (g == 0 && wave == 0) {
+#pragma unroll
+      for (int j = 0; j < D / kWave; ++j) {
+        const size_t idx = static_cast<size_t>(bh) * D + lane + kWave * j;
+        if (OUT_F32)
+          static_cast<float *>(o)[idx] = 0.f;
+        else
+          static_cast<_Float16 *>(o)[idx] = static_cast<_Float16>(0.f);
+      }
+    }
+    return;
+  }
+  const int group_rows = W * chunk;
+  const int n_live = (len + group_rows - 1) / group_rows;  // groups with rows
+  if (g >= n_live) return;
+
+  const int sub = lane / RowGeo<D>::kLanesPerRow;
+  const int slice = lane % RowGeo<D>::kLanesPerRow;
+  float m = kNegBig, l = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  const int begin = (g * W + wave) * chunk;
+  if (begin < len) {
+    const int end = min(len, begin + chunk);
+    const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
+    const _Float16 *kp = k_cache + head_off;
+    const _Float16 *vp = v_cache + head_off;
+    constexpr int kStepRows = RowGeo<D>::kRowsPerGroup * kGroupsPerStep;
+    RowSlotsT<kGroupsPerStep> cur, nxt;
+    int row0 = begin;
+    load_slots<D>(cur, kp, vp, row0, end, sub, slice);
+    half2 qh[4];
+    load_query<D>(q, bh, slice, qh);
+    for (;;) {
+      const int next0 = row0 + kStepRows;
+      const bool more = next0 < end;
+      if (more) load_slots<D>(nxt, kp, vp, next0, end, sub, slice);
+      consume_slots<D>(cur, qh, qscale, row0, end, sub, m, l, acc);
+      if (!more) break;
+      cur = nxt;
+      row0 = next0;
+    }
+  }
+  // Merge the row groups of the wave, then the W waves through LDS.
+#pragma unroll
+  for (int off = RowGeo<D>::kLanesPerRow; off < kWave; off <<= 1) {
+    const float mb = __shfl_xor(m, off);
+    const float lb = __shfl_xor(l, off);
+    float accb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) accb[e] = __shfl_xor(acc[e], off);
+    merge_state(m, l, acc, mb, lb, accb);
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_acc[wave][slice * 8 + e] = acc[e];
+    if (slice == 0) {
+      s_ml[wave][0] = m;
+      s_ml[wave][1] = l;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mg = s_ml[0][0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) mg = fmaxf(mg, s_ml[w][0]);
+  float lg = 0.f, ag[D / kWave];
+#pragma unroll
+  for (int j = 0; j < D / kWave; ++j) ag[j] = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const float f = fast_exp2(s_ml[w][0] - mg);  // empty waves: l = 0, acc = 0
+    lg = fmaf(s_ml[w][1], f, lg);
+#pragma unroll
+    for (int j = 0; j < D / kWave; ++j) ag[j] = fmaf(s_acc[w][lane + kWave * j], f, ag[j]);
+  }
+  // Publish the group partial, wait until it is stored, then count it.
+  const size_t slot = static_cast<size_t>(bh) * n_groups + g;
+#pragma unroll
+  for (int j = 0; j < D / kWave; ++j) store_coherent(part_acc + slot * D + lane + kWave * j, ag[j]);
+  if (lane == 0) {
+    store_coherent(part_ml + slot * 2, mg);
+    store_coherent(part_ml + slot * 2 + 1, lg);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  unsigned ticket = 0;
+  if (lane == 0)
+    ticket = __hip_atomic_fetch_add(counters + bh, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __shfl(ticket, 0);
+  if (static_cast<int>(ticket) != n_live - 1) return;
+  merge_partials_wave<D, OUT_F32>(part_acc, part_ml, static_cast<size_t>(bh) * n_groups, n_live,
+                                  o, static_cast<size_t>(bh), lane);
+  if (lane == 0)
+    __hip_atomic_store(counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Pass 2 (decode.cu:143-175): log-sum-exp merge of the partials of one
 // (b, h). Only the ceil(len / chunk) chunks that hold rows are read (the
 // reference skips the others through l <= 0); a sequence with no rows
@@ -295,17 +508,6 @@ __global__ __launch_bounds__(kSplitThreads) void decode_split_kernel(
 // them. The loads of the common case (seq_len, the first 64 (m, l) pairs
 // and the first 8 partial rows) are all issued before any of them is used,
 // so the pass costs about one memory round trip.
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
-  return x;
-}
-
 // D threads: lane = threadIdx.x % 64 runs the per-chunk statistics (each wave
 // of a 128-thread block computes them for itself), dim = threadIdx.x is the
 // head dim it accumulates.
@@ -856,6 +1058,38 @@ bool use_bh_path(int batch, int heads, int max_seq) {
   return cu > 0 && (static_cast<long long>(batch) * heads >= cu || max_seq <= kBhShortCache);
 }
 
+// Counter slot of g_merge_counters for the current device and `stream`,
+// claimed on first use and kept; nullptr (the two-launch path) when the
+// (b, h) count exceeds a slot or every slot is taken.
+unsigned *merge_counters(hipStream_t stream, size_t n_bh) {
+  if (n_bh > static_cast<size_t>(kCountersPerSlot)) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  struct Owner {
+    int dev;
+    hipStream_t stream;
+  };
+  static std::mutex mu;
+  static unsigned *base[kMaxDevices];
+  static bool looked_up[kMaxDevices];
+  static Owner owner[kCounterSlots];
+  static int n_used = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!looked_up[dev]) {
+    looked_up[dev] = true;
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_merge_counters)) == hipSuccess)
+      base[dev] = static_cast<unsigned *>(p);
+  }
+  if (base[dev] == nullptr) return nullptr;
+  for (int i = 0; i < n_used; ++i)
+    if (owner[i].dev == dev && owner[i].stream == stream)
+      return base[dev] + static_cast<size_t>(i) * kCountersPerSlot;
+  if (n_used == kCounterSlots) return nullptr;
+  owner[n_used] = {dev, stream};
+  return base[dev] + static_cast<size_t>(n_used++) * kCountersPerSlot;
+}
+
 // Queries per wave of the grouped pass: the largest divisor of the group
 // that fits the 32 columns of one MFMA tile.
 int group_queries(int group) {
@@ -944,6 +1178,41 @@ int launch_valu_decode(const void *q, const void *k_cache, const void *v_cache,
   const unsigned split_blocks =
       static_cast<unsigned>((n_units + waves_per_block - 1) / waves_per_block);
 
+  // One launch when a counter slot is free: each group of W waves merges
+  // in LDS and the last group of a (b, h) merges the groups (W = 4 for
+  // chunks of up to 256 rows, where the per-chunk merge traffic and counter
+  // contention dominate; 2 for longer chunks, where more blocks stream).
+  // Else the split pass, then the merge pass.
+  unsigned *const counters = merge_counters(stream, bh);
+  if (counters != nullptr) {
+    const int w = split_size <= 256 ? 4 : 2;
+    const int n_groups = (n_splits + w - 1) / w;
+    const unsigned blocks = static_cast<unsigned>(bh * n_groups);
+    const float qs = scale * kLog2e;
+    const auto *qp = static_cast<const _Float16 *>(q);
+    const auto *kp = static_cast<const _Float16 *>(k_cache);
+    const auto *vp = static_cast<const _Float16 *>(v_cache);
+    if (w == 4) {
+      if (out_f32)
+        hipLaunchKernelGGL((decode_split_fused_kernel<D, true, 4>), dim3(blocks), dim3(4 * kWave),
+                           0, stream, qp, kp, vp, seq_lens, part_acc, part_ml, heads, max_seq,
+                           n_groups, split_size, qs, counters, o);
+      else
+        hipLaunchKernelGGL((decode_split_fused_kernel<D, false, 4>), dim3(blocks), dim3(4 * kWave),
+                           0, stream, qp, kp, vp, seq_lens, part_acc, part_ml, heads, max_seq,
+                           n_groups, split_size, qs, counters, o);
+    } else {
+      if (out_f32)
+        hipLaunchKernelGGL((decode_split_fused_kernel<D, true, 2>), dim3(blocks), dim3(2 * kWave),
+                           0, stream, qp, kp, vp, seq_lens, part_acc, part_ml, heads, max_seq,
+                           n_groups, split_size, qs, counters, o);
+      else
+        hipLaunchKernelGGL((decode_split_fused_kernel<D, false, 2>), dim3(blocks), dim3(2 * kWave),
+                           0, stream, qp, kp, vp, seq_lens, part_acc, part_ml, heads, max_seq,
+                           n_groups, split_size, qs, counters, o);
+    }
+    return check_hip(hipGetLastError(), "decode_split_fused_kernel launch");
+  }
   hipLaunchKernelGGL((decode_split_kernel<D>), dim3(split_blocks),
                      dim3(waves_per_block * kWave), 0, stream,
                      static_cast<const _Float16 *>(q),

@@ -371,6 +371,26 @@ def test_decode_whole_sequence_path_takes_no_workspace():
     assert lib.fa_decode_workspace_bytes(1, 12, 4096, 0) > 0
 
 
+def test_decode_split_path_agrees_across_many_streams():
+    """The split-K path runs as one launch while a per-stream counter slot is
+    free (64 per process) and as the split + merge launches beyond that: 70
+    streams cover both, and every result agrees with the default stream's
+    (fp32 output, summation order only) and with the oracle."""
+    q, k, v, lens = oracle.make_decode_inputs(1, 12, 4096, seed=26)
+    ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    want = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    assert np.abs(want.cpu().numpy() - ref).max() <= BOUND
+    streams = [torch.cuda.Stream() for _ in range(70)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            got = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+        s.synchronize()
+        assert (got - want).abs().max().item() <= 1e-6
+
+
 def test_decode_whole_sequence_split_invariance_fp32():
     q, k, v, lens = oracle.make_decode_inputs(32, 10, 1500, seed=22,
                                               lens=_ragged_lens(32, 1500, seed=23))
