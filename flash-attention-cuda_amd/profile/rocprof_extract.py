@@ -107,39 +107,43 @@ def demangle(name: str) -> str:
     return _demangle_nested(name) or name
 
 
-def _depths(name: str):
-    """(index, char, template depth before the char) over a name."""
+def _mask_templates(text: str) -> str:
+    """`text` with every character between a template's outer brackets
+    replaced by '.', nested brackets included; the outer '<' and '>' stay.
+    The result has the length of `text`, so an index found by a plain
+    string search in it (which then only sees top-level characters) is an
+    index into `text`."""
+    out = []
     depth = 0
-    for i, ch in enumerate(name):
-        if ch == ">":
-            depth = max(0, depth - 1)
-        yield i, ch, depth
+    for ch in text:
         if ch == "<":
+            out.append("<" if depth == 0 else ".")
             depth += 1
+        elif ch == ">" and depth > 0:
+            depth -= 1
+            out.append(">" if depth == 0 else ".")
+        else:
+            out.append("." if depth > 0 else ch)
+    return "".join(out)
 
 
 def short_kernel_name(name: str) -> str:
     """`void fa::(anonymous namespace)::prefill_kernel<true, false>(...)` ->
-    `prefill_kernel<true, false>`. Template arguments stay (they tell the
-    causal and full prefill instantiations apart); the argument list, a
-    leading return type and namespace qualifiers outside the template
-    brackets go. Mangled names are demangled first."""
-    name = demangle(name.strip()).replace("(anonymous namespace)::", "")
-    for i, ch, depth in _depths(name):
-        if ch == "(" and depth == 0:
-            name = name[:i]
-            break
-    name = name.strip()
-    start = 0
-    for i, ch, depth in _depths(name):
-        if ch == " " and depth == 0:
-            start = i + 1
-    name = name[start:]
-    start = 0
-    for i, ch, depth in _depths(name):
-        if ch == ":" and depth == 0 and name[i:i + 2] == "::":
-            start = i + 2
-    return name[start:].strip() or "kernel"
+    `prefill_kernel<true, false>`: the kernel's own name with its template
+    arguments (they tell the instantiations apart). The parameter list, the
+    return type and the qualifiers in front of the name are cut at their
+    top-level '(', ' ' and '::' (those inside template arguments stay).
+    Mangled names are demangled first."""
+    text = demangle(name.strip()).replace("(anonymous namespace)::", "")
+    top = _mask_templates(text)
+    paren = top.find("(")
+    if paren >= 0:
+        text, top = text[:paren], top[:paren]
+    text = text.rstrip()
+    top = top[:len(text)]
+    qualifier = top.rfind("::")
+    cut = max(top.rfind(" ") + 1, qualifier + 2 if qualifier >= 0 else 0)
+    return text[cut:].strip() or "kernel"
 
 
 def read_kernel_stats(path: str) -> dict:

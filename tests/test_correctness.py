@@ -36,7 +36,8 @@ def rand(*shape, seed=None, _state={}):
 
 
 def sdpa_reference(q, k, v, causal, scale=SCALE):
-    """fp32 attention on upcast inputs, cast back to fp16."""
+    """Prefill oracle: an explicit masked softmax per (b, h) in fp32 on the
+    upcast inputs, rounded back to fp16 at the end."""
     out = torch.empty_like(q)
     for b in range(q.shape[0]):
         qf, kf, vf = q[b].float(), k[b].float(), v[b].float()
@@ -50,7 +51,8 @@ def sdpa_reference(q, k, v, causal, scale=SCALE):
 
 
 def decode_reference(q, k_cache, v_cache, seq_lens, scale=SCALE):
-    """fp32 single-query attention over the valid part of each cache."""
+    """Decode oracle: each query attends, in fp32, to cache rows [0, len)
+    of its own sequence only."""
     out = torch.empty_like(q)
     for b in range(q.shape[0]):
         n = int(seq_lens[b])
@@ -86,7 +88,7 @@ def test_prefill_matches_sdpa(batch, heads, seq, causal):
 @pytest.mark.parametrize("seq", [1, 37, 65, 130, 1023])
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_handles_ragged_sequence_lengths(seq, causal):
-    """Sequence lengths that are not a multiple of the tile size."""
+    """Sequence lengths that leave a partial last tile (ragged tails)."""
     q = rand(2, 5, seq, HEAD_DIM, seed=1)
     k = rand(2, 5, seq, HEAD_DIM)
     v = rand(2, 5, seq, HEAD_DIM)
@@ -104,7 +106,8 @@ def test_prefill_handles_ragged_sequence_lengths(seq, causal):
 
 @pytest.mark.parametrize("position", [1, 17, 511, 1024, 2047])
 def test_decode_matches_causal_prefill_row(position):
-    """Decoding position t must reproduce row t of the causal prefill output."""
+    """A decode step at cache length t + 1 sees exactly what causal prefill
+    row t sees, so the two outputs agree."""
     batch, heads, seq = 2, 12, 2048
     q = rand(batch, heads, seq, HEAD_DIM, seed=2)
     k = rand(batch, heads, seq, HEAD_DIM)
@@ -129,7 +132,7 @@ def test_decode_matches_causal_prefill_row(position):
     ],
 )
 def test_decode_ragged_batch(seq_lens):
-    """Every sequence in the batch has a different cache occupancy."""
+    """One batch, four different fill levels per cache (1 row to full)."""
     batch, heads, cache = len(seq_lens), 8, 4096
     q = rand(batch, heads, 1, HEAD_DIM, seed=3)
     k_cache = rand(batch, heads, cache, HEAD_DIM)
@@ -144,7 +147,8 @@ def test_decode_ragged_batch(seq_lens):
 
 @pytest.mark.parametrize("cache", [1, 63, 512, 513, 2048])
 def test_decode_cache_lengths(cache):
-    """Cache sizes around the split boundary."""
+    """Cache lengths on both sides of the 512-row path switch (whole-sequence
+    kernel below, split-K above), down to a single row."""
     batch, heads = 3, 12
     q = rand(batch, heads, 1, HEAD_DIM, seed=4)
     k_cache = rand(batch, heads, cache, HEAD_DIM)
@@ -159,7 +163,9 @@ def test_decode_cache_lengths(cache):
 
 @pytest.mark.parametrize("cache", [512, 1024, 2048])
 def test_decode_is_invariant_to_split_size(cache):
-    """The split-K chunk size is a scheduling choice, not a numerical one."""
+    """Forcing any chunk size changes only how the work is partitioned: every
+    forced result stays within the bound of the reference and close to the
+    automatically chunked one."""
     batch, heads = 2, 12
     q = rand(batch, heads, 1, HEAD_DIM, seed=7)
     k_cache = rand(batch, heads, cache, HEAD_DIM)
@@ -177,7 +183,8 @@ def test_decode_is_invariant_to_split_size(cache):
 
 
 def test_decode_split_choice_targets_the_device():
-    """The chosen chunk fills the GPU when the shape allows it."""
+    """The automatic chunk gives at least 2 x CUs units whenever some chunk
+    can, and is then the coarsest one that does; otherwise the finest."""
     sms = torch.cuda.get_device_properties(0).multi_processor_count
     target = 2 * sms
 
@@ -186,13 +193,13 @@ def test_decode_split_choice_targets_the_device():
         assert split in (128, 256, 512, 1024)
         blocks = batch * heads * -(-seq // split)
         if blocks >= target:
-            # and it is the largest such chunk: doubling it must fall short
+            # coarsest qualifying chunk: twice as long would leave too few units
             if split < 1024:
                 assert batch * heads * -(-seq // (split * 2)) < target
         else:
             assert split == 128
 
-    # Shapes too small to reach the target fall back to the finest split.
+    # No chunk reaches the target on a small shape: the finest one is used.
     assert flashattn_cuda.choose_decode_split(512, 1, 12, target) == 128
 
 
