@@ -17,6 +17,7 @@ them, and torch is only needed for the thin binding layer.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -124,6 +125,58 @@ def build_extension() -> str:
     _run(cmd)
     os.replace(tmp, out)
     return out
+
+
+# --- m0 check ------------------------------------------------------------------
+# The direct global->LDS loads (global_to_lds16 in csrc/mfma_tile.h) set m0,
+# the LDS base of the load, from inline asm. The backend reserves m0 and does
+# not see that write, so the kernels stay correct only while nothing else in
+# them defines or reads m0. These checks run on the gfx950 assembly.
+
+_M0_IMPLICIT_READERS = ("s_movrel", "v_movrel", "s_sendmsg", "ds_gws", "ds_append",
+                        "ds_consume", "v_interp", "ds_read_addtid", "ds_write_addtid",
+                        "s_ttracedata", "buffer_load_lds")
+_M0_WRITE = re.compile(r"s_mov_b32 m0, s\d+$")
+
+
+def m0_problems(asm: str) -> list:
+    """Every instruction in `asm` (AMDGPU assembly) that defines or reads m0
+    other than the global_to_lds16 pattern `s_mov_b32 m0, sN` [s_nop ...]
+    `global_load_lds_dwordx4`, and every global_load_lds without that write
+    right before it."""
+    code = []
+    for raw in asm.splitlines():
+        ins = raw.split(";", 1)[0].strip()
+        if ins and not ins.startswith(".") and not ins.endswith(":"):
+            code.append(ins)
+    problems = []
+    for i, ins in enumerate(code):
+        op = ins.split()[0]
+        if op.startswith("global_load_lds"):
+            j = i - 1
+            while j >= 0 and code[j].startswith("s_nop"):
+                j -= 1
+            if j < 0 or not _M0_WRITE.match(code[j]):
+                problems.append(f"global_load_lds without its m0 write: {ins}")
+        elif re.search(r"\bm0\b", ins):
+            j = i + 1
+            while j < len(code) and code[j].startswith("s_nop"):
+                j += 1
+            if not (_M0_WRITE.match(ins) and j < len(code)
+                    and code[j].split()[0].startswith("global_load_lds")):
+                problems.append(f"m0 outside a global_load_lds sequence: {ins}")
+        elif op.startswith(_M0_IMPLICIT_READERS) or (op.startswith("buffer_load") and " lds" in ins):
+            problems.append(f"reads m0 implicitly: {ins}")
+    return problems
+
+
+def device_assembly(src: str, out_dir: str) -> str:
+    """gfx950 assembly of one csrc/ source, built with the library's flags."""
+    out = os.path.join(out_dir, os.path.basename(src).replace(".hip", ".s"))
+    _run([_hipcc(), *HIPCC_FLAGS, "--cuda-device-only", "-S", os.path.join(CSRC, src),
+          "-o", out])
+    with open(out, encoding="utf-8") as handle:
+        return handle.read()
 
 
 def build(verbose: bool = True) -> None:

@@ -41,8 +41,9 @@ __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
 // tracks completion itself with explicit vmcnt waits.
 // m0 is listed as clobbered for the reader; the compiler treats m0 as a
 // reserved register and does not track it (hence the silenced warning), which
-// is safe because nothing else in the kernels that use it reads m0 (checked in
-// the generated ISA: every m0 write is the one in this function).
+// is safe only while nothing else in the kernels defines or reads m0:
+// tests/test_build_checks.py builds the gfx950 assembly of prefill.hip and
+// decode.hip and fails on any other m0 use (build.py m0_problems).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void global_to_lds16(const void *src, const void *lds_dst) {
