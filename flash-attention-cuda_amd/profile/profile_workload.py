@@ -40,7 +40,8 @@ WORKLOADS = {
                         "flop", 4.0 * 4 * 12 * 1024 * 1024 * 64),
     "prefill_c3_d128": ("config 3 shape at head_dim 128: causal prefill B=1 H=14 S=4096 D=128",
                         "prefill_kernel<128, true", "flop", 4.0 * 14 * 4096 * 4096 * 128 / 2),
-    "decode_c4": ("config 4: decode B=1 H=12 L=4096 (split-K + merge)", "decode_split_kernel",
+    "decode_c4": ("config 4: decode B=1 H=12 L=4096 (split-K, merged in the same launch)",
+                  "decode_split_fused_kernel",
                   "byte", 2 * 12 * 64 * 2 * 4096 + 2 * 12 * 64 * 2 + 4),
     "decode_c5": ("config 5: ragged decode B=32 H=14 Lmax=4096, lens U[1,4096] seed 0",
                   "decode_bh_kernel", "byte", 2 * 14 * 64 * 2 * 73374 + 2 * 32 * 14 * 64 * 2 + 128),

@@ -51,8 +51,18 @@ def _parity_record():
     path = os.environ.get("FA_PARITY_RECORD")
     if not path or not _RECORD:
         return
-    lines = ["| Configuration | fp32-output error | fp16-output error | fp16 rounding floor | "
-             "flat 2.44e-4 on fp16 asserted |", "|---|---|---|---|---|"]
+    lines = [
+        "# Parity of the BASELINE configurations (MI355X)", "",
+        "Written by the GPU parity tests (`tests/test_parity.py`) on an MI355X with", "",
+        "    FA_PARITY_RECORD=profiles/parity.md python -m pytest tests/test_parity.py -m gpu "
+        "-k \"baseline or c4 or c5\"", "",
+        "Inputs: the BASELINE configurations drawn on the CPU (`oracle.make_prefill_inputs` / "
+        "`oracle.make_decode_inputs`, the seeds of the tests); reference: the float64 oracle. "
+        "Contract: fp32-output error <= 2.44e-4 everywhere; fp16-output error <= 2.44e-4 "
+        "wherever the fp16 rounding floor max|fp16(ref) - ref| is below it, and within "
+        "2.44e-4 of half an fp16 ulp elsewhere.", "",
+        "| Configuration | fp32-output error | fp16-output error | fp16 rounding floor | "
+        "flat 2.44e-4 on fp16 asserted |", "|---|---|---|---|---|"]
     for label, e32, e16, floor, flat in _RECORD:
         lines.append(f"| {label} | {e32:.3e} | {e16:.3e} | {floor:.3e} | {'yes' if flat else 'no (floor above the bound)'} |")
     with open(path, "w") as f:
