@@ -8,7 +8,13 @@
 //  * B * H < compute units (too few (b, h) pairs to fill the chip): the
 //    reference's split-K scheme. The cache rows of each (b, h) are cut into
 //    chunks of `chunk` rows, each chunk yields a partial (m, l, acc[64]) in
-//    the workspace, and a merge kernel combines them.
+//    the workspace, and the partials are combined in the same launch
+//    (decode_split_fused_kernel): groups of W waves pre-merge in LDS, publish
+//    one partial per group, and bump a per-(b, h) counter; the group that
+//    arrives last merges the rest and resets the counter. Counters live in a
+//    zero-initialised device array, one slot per (device, stream); a call
+//    that finds no free slot takes the two-launch path (split kernel, then
+//    merge kernel).
 //  * B * H >= compute units, or a cache of at most 512 rows: one 8-wave
 //    block per (b, h) folds the whole sequence (decode_bh_kernel below),
 //    merging its waves through LDS, so no partials reach HBM and there is no
@@ -34,7 +40,7 @@
 //  * head_dim 128 keeps the lane -> 16 B mapping: 16 lanes per row, 4 rows
 //    per load instruction, a 4-step DPP sum (RowGeo<D>).
 //  * The per-lane online-softmax states are merged across the row groups of
-//    the wave with shuffles, and across chunks by the merge kernel.
+//    the wave with shuffles, and across chunks as described above.
 //  * Grouped-query attention (H_kv < H K/V heads) does not use these VALU
 //    passes: decode_group_kernel (below) runs the split pass on the matrix
 //    cores with up to 32 query heads of one K/V head per wave, so each cache
