@@ -87,6 +87,30 @@ __device__ __forceinline__ floatx16 mfma(const half8 &a, const half8 &b,
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Row sums of P^T fragments on the matrix cores.
+// v_mfma_f32_16x16x32_f16 (lane l: A[l % 16][8 (l / 16) + i],
+// B[8 (l / 16) + i][l % 16], result rows 4 (l / 16) + j of column l % 16)
+// reads a 32x32x16 B fragment (lane l: query l % 32, keys 8 (l / 32) + i of
+// a 16-key step) as B[k][n] with k-group l / 16 and column l % 16: k-groups
+// 0 and 2 hold query n, k-groups 1 and 3 query n + 16. A selector with ones
+// in rows {0, 8} over k-groups {0, 2} and in rows {4, 12} over k-groups
+// {1, 3} therefore puts the 16-key sum of query l % 32 into result element 0
+// of lane l, for all 64 lanes (rows 0, 4, 8, 12 are element 0 of lane groups
+// 0-3); elements 1-3 stay zero.
+__device__ __forceinline__ floatx4 mfma16(const half8 &a, const half8 &b, const floatx4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half8 rowsum_selector(int lane) {
+  const int m = lane & 15;
+  const bool odd_group = (lane >> 4) & 1;
+  const bool on = odd_group ? (m == 4 || m == 12) : (m == 0 || m == 8);
+  const _Float16 one = static_cast<_Float16>(on ? 1.0f : 0.0f);
+  half8 s;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s[i] = one;
+  return s;
+}
+
 // Per-lane LDS offsets (in halves, relative to a tile) of every fragment a
 // wave reads from a tile; loop invariant.
 struct FragOffsets {

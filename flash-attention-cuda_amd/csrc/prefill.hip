@@ -43,9 +43,10 @@
 // Main loop (tiles that need no mask), per wave and step k of its half:
 //   wait for tile k+2 and this wave's LDS reads -> barrier -> issue the loads
 //   of tile k+4 ->
-//   O *= alpha_{k-1} (only where a row's max rose) -> row max of S_k ->
-//   { QK(k+1) and PV(k-1) on the matrix cores } interleaved with
-//   { exp / pack / row sum of S_k on the VALU } ->
+//   charge the rounded mass of P_{k-2} -> O *= alpha_{k-1} (only when m
+//   moved) -> row max of S_k ->
+//   { QK(k+1), PV(k-1) and the row sums of P_{k-1} on the matrix cores }
+//   interleaved with { exp / pack of S_k on the VALU } ->
 //   LDS reads of the next step's fragments (K_{k+2}, V_k), which land while
 //   the next barrier and row max run.
 //   S and P are double-buffered (the loop is unrolled by two), so the MFMAs of
@@ -74,25 +75,35 @@
 //   16-byte load, and the key order of P^T is the accumulator's own.
 //
 // Softmax: log2 domain, p = exp2(s * c - m) with c = |scale| * log2(e) (a
-// negative scale is folded into Q by an exact fp16 negation). m is the exact
-// running max, so the dominant key of a row always enters the PV product as
-// P = 1 exactly. The row sum l is accumulated from the same fp16 P values the
-// PV product consumes (v_dot2_f32_f16), so the weights that multiply V sum to
-// exactly the l they are divided by.
+// negative scale is folded into Q by an exact fp16 negation). The row sum l
+// is accumulated from the same fp16 P values the PV product consumes, so the
+// weights that multiply V sum to exactly the l they are divided by: at
+// head_dim 64 on the matrix cores (one v_mfma_f32_16x16x32_f16 per 16-key
+// step against a 0/1 selector, rowsum_mfma), at head_dim 128 per lane with
+// v_dot2_f32_f16.
+// The max m: rows that see >= 1024 keys (head_dim 64) take a lazy max. m
+// moves, to the row's exact running max, only when a tile max exceeds it by
+// more than 8 (log2 units), so P <= 2^8 and O is rescaled on a few steps per
+// item instead of on most of them. Shorter rows, and every row at head_dim
+// 128, keep m at the exact running max (every step where some row's max rose
+// rescales). Whenever a tile sets m, its dominant key enters the PV product
+// as P = 1 exactly.
 //
 // Precision of P: one fp16 rounding of each weight w = p / l moves an output
 // row by about 2^-11 sqrt(sum w^2) times the spread of V, summed over the
-// rounded weights (the P = 1 key is exact and does not count). Rows carried by
+// rounded weights (a P = 1 key is exact and does not count). Rows carried by
 // a few keys therefore need P split into hi + lo fp16 parts, with the PV
 // product issued twice (relative error ~2^-22). Rows that see fewer than 256
 // keys always take the split. Every other row tracks an upper bound of its
 // rounded mass r = sum w^2: per tile, (largest weight) x (weight sum), minus
-// the exact 1 of a tile that sets the running max, rescaled with the max like
-// l. A block with a row whose r / l^2 ends above kRedoRoundedMassAbove (0.08:
-// output error ~2e-4 at the bound, measured on inputs up to 3.4x the N(0,1)
-// logit width) is computed again with split P on every tile. Independent
-// N(0,1) inputs at 1/sqrt(D) stay below 0.065 (rows with 256-383 keys) and
-// below 0.045 beyond, so they take the single-rounding pass only.
+// the exact 1 of a tile whose largest weight is exactly 1, rescaled with m
+// like l. (head_dim 64 takes a tile's weight sum from the row-sum
+// accumulator two steps later, charge_mass.) A block with a row whose
+// r / l^2 ends above kRedoRoundedMassAbove (0.08: output error ~2e-4 at the
+// bound, measured on inputs up to 3.4x the N(0,1) logit width) is computed
+// again with split P on every tile. Independent N(0,1) inputs at 1/sqrt(D)
+// stay below 0.065 (rows with 256-383 keys) and below 0.045 beyond, so they
+// take the single-rounding pass only.
 
 #include <algorithm>
 #include <type_traits>
@@ -122,6 +133,10 @@ constexpr float kRedoRoundedMassAbove = 0.08f;
 // from the scale alone, so the first (single-rounding) pass is skipped.
 constexpr float kSplitAllWidth = 1.5f;
 constexpr float kNegHuge = -3.0e38f;
+// The max that P is taken against moves only when a row's tile max exceeds it
+// by more than this (log2 units), so P <= 2^8 and O is rescaled on few steps.
+constexpr float kLazyMaxSlack = 8.0f;
+constexpr int kLazyMaxRowsFrom = 1024;  // keys a row sees (at least) to take the lazy max
 
 // Tile geometry for head_dim D (64 or 128). A K or V tile is always 8 KiB:
 // 64 keys of 128 B rows for D = 64, 32 keys of 256 B rows for D = 128, so a
@@ -164,12 +179,23 @@ __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
   return *reinterpret_cast<const half8 *>(p);
 }
 
+// head_dim 64 sums P rows on the matrix cores (rowsum_mfma) and takes the
+// lazy max on long rows; head_dim 128, whose loop has no registers to spare,
+// sums them with v_dot2_f32_f16 per lane and keeps the exact running max.
+template <int D>
+constexpr bool kMfmaRowSum = D == 64;
+
+// Per-lane softmax state of one query row. head_dim 64: both lanes of a pair
+// hold the same m, mt, r and row sum (lacc[0]). head_dim 128: m is the exact
+// running max, l and r are this lane's shares of the row's sums.
 template <int D>
 struct SoftmaxState {
-  float m;                      // running max (log2 domain, already scaled by c)
-  float l;                      // this lane's share of the row sum
-  float r;                      // this lane's share of the rounded mass (below)
-  float pm;                     // largest weight of the current tile
+  float m;                      // the max P is taken against (log2 domain, scaled by c)
+  float mt;                     // the row's true running max (log2 domain)
+  float r;                      // rounded-mass bound (below), in units of m
+  float lprev;                  // row sum already charged to r (head_dim 64)
+  float l;                      // this lane's share of the row sum (head_dim 128)
+  floatx4 lacc;                 // row sum on the matrix cores: element 0 (head_dim 64)
   floatx16 o[Geo<D>::kDB];      // O^T accumulators, one per 32-dim block
 };
 
@@ -240,12 +266,28 @@ __device__ __forceinline__ void pv_mfma(const VFrags<D> &v, const half8 (&p)[Geo
     for (int db = 0; db < Geo<D>::kDB; ++db) o[db] = mfma(v.f[ks][db], p[ks], o[db]);
 }
 
-// New running max for one tile; returns alpha, the factor that rescales the
-// previous O and l (l is rescaled here, O by the caller).
+// Row sums of a tile's P^T fragments, on the matrix cores (one
+// v_mfma_f32_16x16x32_f16 per 16-key step, see rowsum_selector): element 0
+// of lacc gathers the sum of the same fp16 P values that the PV product
+// consumes, for the lane's own query.
+template <int D>
+__device__ __forceinline__ void rowsum_mfma(const half8 &sel, const half8 (&p)[Geo<D>::kKS],
+                                            floatx4 &lacc) {
+  if constexpr (!kMfmaRowSum<D>) return;
+#pragma unroll
+  for (int ks = 0; ks < Geo<D>::kKS; ++ks) lacc = mfma16(sel, p[ks], lacc);
+}
+
+// Row max of one tile and the lazy update of m. Returns whether the wave
+// rescales (wave-uniform): m moves, to the row's exact running max, only when
+// some row of the wave has a tile max more than kLazyMaxSlack above its m;
+// alpha (set then) rescales the previous O, row sum and rounded mass. pm is
+// the tile's largest weight in units of the (new) m.
 // MASK: keys past the end or above the causal diagonal become -inf.
 template <bool CAUSAL, bool MASK, int D>
-__device__ __forceinline__ float tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, float c_scale,
-                                          SoftmaxState<D> &st) {
+__device__ __forceinline__ bool tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, float c_scale,
+                                         float slack, SoftmaxState<D> &st, float &alpha,
+                                         float &pm) {
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < Geo<D>::kKB; ++kb) {
@@ -257,34 +299,41 @@ __device__ __forceinline__ float tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, f
     }
   }
   mx = max_lane_pair(mx);
-  float mx_c, m_new, alpha;
+  float mx_c;
   {
-    // No contraction here: with mx_c rounded once, a tile that sets the
-    // running max gets largest weight exp2(0) = 1 exactly.
+    // No contraction: with mx_c rounded once, a tile that sets m gets
+    // largest weight exp2(0) = 1 exactly.
 #pragma clang fp contract(off)
     mx_c = mx * c_scale;
-    m_new = fmaxf(st.m, mx_c);
-    alpha = fast_exp2(st.m - m_new);
-    st.pm = fast_exp2(mx_c - m_new);
   }
-  st.m = m_new;
-  st.l *= alpha;
-  st.r *= alpha * alpha;
-  return alpha;
+  st.mt = fmaxf(st.mt, mx_c);
+  const bool rescale = __builtin_amdgcn_ballot_w64(mx_c > st.m + slack) != 0;
+  alpha = 1.0f;
+  if (rescale) {
+    alpha = fast_exp2(st.m - st.mt);
+    st.m = st.mt;
+    if constexpr (!kMfmaRowSum<D>) {
+      st.l *= alpha;
+      st.r *= alpha * alpha;
+    }
+  }
+  pm = fast_exp2(mx_c - st.m);
+  return rescale;
 }
 
-// P^T fragments (hi [+ lo]) of one tile and the row-sum update. Without the
-// lo part, the rounded mass r grows by (largest weight) x (weight sum) of the
-// tile, an upper bound on the tile's squared weights; a weight equal to the
-// running max is exactly 1 in fp16 and is left out (half of it in each lane
-// of the pair, since only their sum is used).
+// P^T fragments (hi [+ lo]) of one tile. head_dim 128 also adds the tile to
+// its row-sum share and, with one rounding of P, its rounded mass: the tile's
+// largest weight pm times its weight sum, minus the exact 1 of a tile whose
+// largest weight is the running max (half of it in each lane of the pair,
+// since only their sum is used).
 template <bool MASK, bool SPLIT, int D>
 __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float c_scale,
-                                         SoftmaxState<D> &st, half8 (&p_hi)[Geo<D>::kKS],
+                                         float pm, SoftmaxState<D> &st,
+                                         half8 (&p_hi)[Geo<D>::kKS],
                                          half8 (&p_lo)[Geo<D>::kKS]) {
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-  const float m_use = st.m;
   float lsum = 0.f;
+  const float m_use = st.m;
 #pragma unroll
   for (int ks = 0; ks < Geo<D>::kKS; ++ks) {
     const int kb = ks >> 1, h = ks & 1;
@@ -300,40 +349,60 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float
       const half2 hi2 = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
       p_hi[ks][t] = hi2[0];
       p_hi[ks][t + 1] = hi2[1];
-      lsum = __builtin_amdgcn_fdot2(hi2, ones, lsum, false);
+      if constexpr (!kMfmaRowSum<D>) lsum = __builtin_amdgcn_fdot2(hi2, ones, lsum, false);
       if (SPLIT) {
         const half2 lo2 = {static_cast<_Float16>(p0 - static_cast<float>(hi2[0])),
                            static_cast<_Float16>(p1 - static_cast<float>(hi2[1]))};
         p_lo[ks][t] = lo2[0];
         p_lo[ks][t + 1] = lo2[1];
-        lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
+        if constexpr (!kMfmaRowSum<D>) lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
       }
     }
   }
-  st.l += lsum;
-  if (!SPLIT) st.r = fmaf(-0.5f, floorf(st.pm), fmaf(st.pm, lsum, st.r));
+  if constexpr (!kMfmaRowSum<D>) {
+    st.l += lsum;
+    if (!SPLIT) st.r = fmaf(-0.5f, floorf(pm), fmaf(pm, lsum, st.r));
+  }
 }
 
-// O *= alpha when the max of any row of the wave rose (wave-uniform branch;
-// alpha is exactly 1 otherwise).
+// O, the row sum and the rounded mass follow a move of m (wave-uniform branch).
 template <int D>
-__device__ __forceinline__ void rescale_o(SoftmaxState<D> &st, float alpha) {
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+__device__ __forceinline__ void rescale_o(SoftmaxState<D> &st, float alpha, bool rescale) {
+  if (rescale) {
 #pragma unroll
     for (int db = 0; db < Geo<D>::kDB; ++db)
 #pragma unroll
       for (int a = 0; a < 16; ++a) st.o[db][a] *= alpha;
+    if constexpr (kMfmaRowSum<D>) {
+      st.lacc[0] *= alpha;
+      st.lprev *= alpha;
+      st.r *= alpha * alpha;
+    }
   }
 }
 
-// Scheduling pipeline for one main step: each of its 16 MFMAs followed by a
+// Rounded mass: the row-sum growth since the last charge, times an upper bound
+// of the largest weight among the tiles it came from (a pm taken before a
+// later move of m only overstates it), is an upper bound of those tiles'
+// squared weights.
+template <int D>
+__device__ __forceinline__ void charge_mass(SoftmaxState<D> &st, float pm) {
+  if constexpr (!kMfmaRowSum<D>) return;
+  const float l_now = st.lacc[0];
+  st.r = fmaf(pm, l_now - st.lprev, st.r) - (pm == 1.0f ? 1.0f : 0.0f);
+  st.lprev = l_now;
+}
+
+// Scheduling pipeline for one main step: each of its MFMAs followed by a
 // group of VALU instructions (the softmax of the other tile), then a hard
 // scheduling boundary so no compute sinks below the next step's barrier.
+template <int D>
 __device__ __forceinline__ void interleave_step() {
+  constexpr int kMfmas = 16 + Geo<D>::kKS;  // QK + PV + row sums
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < kMfmas; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -348,23 +417,26 @@ __device__ __forceinline__ void keep(const half8 (&p)[N]) {
 }
 
 // Plain (non-pipelined) step for masked / short-row tiles: QK, softmax with
-// mask and split P, PV issued twice.
+// mask and split P, PV and the row sums issued for both parts.
 template <bool CAUSAL, int D>
 __device__ __forceinline__ void slow_step(const KFrags<D> &kf, const VFrags<D> &vf,
-                                          const half8 (&qf)[Geo<D>::kDS], int key0, int seq,
-                                          int my_q, int lane, float c_scale,
-                                          SoftmaxState<D> &st) {
+                                          const half8 (&qf)[Geo<D>::kDS], const half8 &sel,
+                                          int key0, int seq, int my_q, int lane, float c_scale,
+                                          float slack, SoftmaxState<D> &st) {
   floatx16 s[Geo<D>::kKB];
   qk_mfma<D>(kf, qf, s);
   // Element a of key block kb holds key key0 + kb*32 + 8 (a/4) + 4 g + a%4;
   // it is visible iff that offset is <= lim (last visible key - key0 - 4 g).
   const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
-  const float alpha = tile_max<CAUSAL, true, D>(s, lim, c_scale, st);
-  rescale_o(st, alpha);
+  float alpha, pm;
+  const bool rescale = tile_max<CAUSAL, true, D>(s, lim, c_scale, slack, st, alpha, pm);
+  rescale_o(st, alpha, rescale);
   half8 p_hi[Geo<D>::kKS], p_lo[Geo<D>::kKS];
-  tile_exp<true, true, D>(s, c_scale, st, p_hi, p_lo);
+  tile_exp<true, true, D>(s, c_scale, pm, st, p_hi, p_lo);
   pv_mfma<D>(vf, p_hi, st.o);
   pv_mfma<D>(vf, p_lo, st.o);
+  rowsum_mfma<D>(sel, p_hi, st.lacc);
+  rowsum_mfma<D>(sel, p_lo, st.lacc);
 }
 
 // The K and V rings of one key half: half h owns tiles 2 k + h (k = 0, 1,
@@ -520,6 +592,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     ring.lds_off[i] = rblock * G::kRowsPerLoad * D;
   }
   const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
+  const half8 sel = rowsum_selector(lane);
 
   // Items are (b, h, 128-row query tile), numbered heaviest (last) query
   // tile first. Block b of the G-block grid (G >= items / 2) takes item b,
@@ -571,6 +644,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
   const int n_main = main_tiles / 2;
   const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
+  // Rows that see many keys take the lazy max; shorter ones keep m at the
+  // exact running max, whose P = 1 key takes no rounding.
+  const float slack =
+      kMfmaRowSum<D> && (CAUSAL ? q0 : seq) >= kLazyMaxRowsFrom ? kLazyMaxSlack : 0.f;
 
   half8 qf[kDS];
   SoftmaxState<D> st;
@@ -615,8 +692,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     }
 
     st.m = kNegHuge;
-    st.l = 0.f;
+    st.mt = kNegHuge;
     st.r = 0.f;
+    st.lprev = 0.f;
+    st.l = 0.f;
+    st.lacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
@@ -638,7 +718,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done
       ring.advance(kk);
-      if (active) slow_step<CAUSAL, D>(kf, vf, qf, key0, seq, my_q, lane, c_scale, st);
+      if (active)
+        slow_step<CAUSAL, D>(kf, vf, qf, sel, key0, seq, my_q, lane, c_scale, slack, st);
     }
   };
   auto merge_halves = [&]() -> float * {
@@ -655,7 +736,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
         for (int i = 0; i < 4; ++i)
           xg[(4 * db + i) * kWave] = {st.o[db][4 * i], st.o[db][4 * i + 1], st.o[db][4 * i + 2],
                                       st.o[db][4 * i + 3]};
-      xg[4 * kDB * kWave] = {st.m, st.l, st.r, 0.f};
+      xg[4 * kDB * kWave] = {st.m, kMfmaRowSum<D> ? st.lacc[0] : st.l, st.r, 0.f};
     }
     __syncthreads();
     if (half == 0) {
@@ -671,7 +752,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) st.o[db][4 * i + e] = st.o[db][4 * i + e] * f0 + o1[e] * f1;
         }
-      st.l = st.l * f0 + mlr[1] * f1;
+      if constexpr (kMfmaRowSum<D>)
+        st.lacc[0] = st.lacc[0] * f0 + mlr[1] * f1;
+      else
+        st.l = st.l * f0 + mlr[1] * f1;
       st.r = st.r * (f0 * f0) + mlr[2] * (f1 * f1);
     }
     return xbase;
@@ -690,42 +774,52 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     half8 p_a[kKS], p_b[kKS], p_unused[kKS];
     KFrags<D> kf;
     VFrags<D> vf;
-    float alpha;
+    // alpha / rescale: the move of m that the next step applies to O before
+    // its PV. pm_a, pm_b: largest weights of the P tiles in p_a, p_b, kept
+    // until their row sums are charged to the rounded mass (charge_mass at the
+    // start of the step after the one that issued their row-sum MFMAs).
+    float alpha, pm_a, pm_b = 0.f;
+    bool rescale;
     read_k(ring.kstage(0), fo, kf);
     qk_mfma(kf, qf, s_a);
     read_k(ring.kstage(1), fo, kf);
 
     // step 0 (no PV yet)
     ring.advance(0);
-    alpha = tile_max<CAUSAL, false>(s_a, 0, c_scale, st);
+    rescale = tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
     qk_mfma(kf, qf, s_b);
-    tile_exp<false, false>(s_a, c_scale, st, p_a, p_unused);
+    tile_exp<false, false>(s_a, c_scale, pm_a, st, p_a, p_unused);
     __builtin_amdgcn_sched_barrier(0);
     read_k(ring.kstage(2), fo, kf);
     read_v(ring.vstage(0), fo, vf);
     kk = 1;
 
     // steps kk (odd: S_kk in s_b, P_{kk-1} in p_a) and kk + 1 (even); kf and
-    // vf hold K_{kk+1} and V_{kk-1}
+    // vf hold K_{kk+1} and V_{kk-1}. At step k the row-sum accumulator holds
+    // P up to k - 2, so charge_mass charges P_{k-2} (pm of the same parity).
     for (; kk + 1 < n_main; kk += 2) {
       ring.advance(kk);
-      rescale_o(st, alpha);
-      alpha = tile_max<CAUSAL, false>(s_b, 0, c_scale, st);
+      charge_mass(st, pm_b);
+      rescale_o(st, alpha, rescale);
+      rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
+      rowsum_mfma<D>(sel, p_a, st.lacc);
       qk_mfma(kf, qf, s_a);
       pv_mfma(vf, p_a, st.o);
-      tile_exp<false, false>(s_b, c_scale, st, p_b, p_unused);
-      interleave_step();
+      tile_exp<false, false>(s_b, c_scale, pm_b, st, p_b, p_unused);
+      interleave_step<D>();
       keep(p_b);
       read_k(ring.kstage(kk + 2), fo, kf);
       read_v(ring.vstage(kk), fo, vf);
 
       ring.advance(kk + 1);
-      rescale_o(st, alpha);
-      alpha = tile_max<CAUSAL, false>(s_a, 0, c_scale, st);
+      charge_mass(st, pm_a);
+      rescale_o(st, alpha, rescale);
+      rescale = tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
+      rowsum_mfma<D>(sel, p_b, st.lacc);
       qk_mfma(kf, qf, s_b);
       pv_mfma(vf, p_b, st.o);
-      tile_exp<false, false>(s_a, c_scale, st, p_a, p_unused);
-      interleave_step();
+      tile_exp<false, false>(s_a, c_scale, pm_a, st, p_a, p_unused);
+      interleave_step<D>();
       keep(p_a);
       read_k(ring.kstage(kk + 3), fo, kf);
       read_v(ring.vstage(kk + 1), fo, vf);
@@ -738,36 +832,53 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // (head_dim 128: its 32-key tiles put two masked tiles in each half's
     // range; the second one takes the plain step below.)
     const bool tail = n_steps >= n_main + 1;
+    // Largest weights of the two P tiles not yet charged: the one whose row
+    // sums the last step issued, and the one still waiting for its PV.
+    float pm_summed = pm_b, pm_pending = pm_a;
     if (kk < n_main) {  // one more (odd) main step; leaves S_{kk+1} in s_b, P_kk in p_a
       ring.advance(kk);
-      rescale_o(st, alpha);
-      alpha = tile_max<CAUSAL, false>(s_b, 0, c_scale, st);
+      charge_mass(st, pm_b);
+      rescale_o(st, alpha, rescale);
+      rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
       if (tail) qk_mfma(kf, qf, s_a);
+      rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
-      tile_exp<false, false>(s_b, c_scale, st, p_a, p_unused);
+      tile_exp<false, false>(s_b, c_scale, pm_b, st, p_a, p_unused);
       read_v(ring.vstage(kk), fo, vf);
       ++kk;
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) s_b[kb] = s_a[kb];
+      pm_summed = pm_a;
+      pm_pending = pm_b;
     }
+    // The last tiles are charged one at a time (each charge waits for the
+    // row-sum MFMAs before it, once per item).
+    charge_mass(st, pm_summed);
     if (tail) {
       ring.advance(kk);
       const int key0 = ring.tile(kk) * kBc;
       const bool active = ring.exists(kk) && key0 < wave_key_end;
-      rescale_o(st, alpha);
+      rescale_o(st, alpha, rescale);
+      rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
+      charge_mass(st, pm_pending);
       if (active) {
         const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
-        alpha = tile_max<CAUSAL, true>(s_b, lim, c_scale, st);
-        tile_exp<true, false>(s_b, c_scale, st, p_a, p_unused);
+        float pm_t;
+        rescale = tile_max<CAUSAL, true>(s_b, lim, c_scale, slack, st, alpha, pm_t);
+        tile_exp<true, false>(s_b, c_scale, pm_t, st, p_a, p_unused);
         read_v(ring.vstage(kk), fo, vf);
-        rescale_o(st, alpha);
+        rescale_o(st, alpha, rescale);
+        rowsum_mfma<D>(sel, p_a, st.lacc);
         pv_mfma(vf, p_a, st.o);
+        charge_mass(st, pm_t);
       }
       ++kk;
     } else {
-      rescale_o(st, alpha);
+      rescale_o(st, alpha, rescale);
+      rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
+      charge_mass(st, pm_pending);
     }
   }
 
@@ -782,8 +893,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // its verdict in its own (already consumed) exchange slot; after the
     // barrier every wave reads all four.
     if (half == 0) {
-      const float l_row = st.l + __shfl_xor(st.l, 32);
-      const float r_row = st.r + __shfl_xor(st.r, 32);
+      const float l_row = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
+      const float r_row = kMfmaRowSum<D> ? st.r : st.r + __shfl_xor(st.r, 32);
       const bool peaky = my_q < seq && r_row > kRedoRoundedMassAbove * l_row * l_row;
       const float verdict = __builtin_amdgcn_ballot_w64(peaky) != 0 ? 1.0f : 0.0f;
       if (lane == 0) xchg[0] = verdict;
@@ -812,7 +923,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     constexpr int kChunksOut = kRowBytes / 16;          // 16-byte chunks per row
     constexpr int kRowsPerStore = kWave / kChunksOut;    // rows per store instruction
     const int g = lane >> 5;
-    const float l_tot = st.l + __shfl_xor(st.l, 32);
+    const float l_tot = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
     const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
     char *stage = reinterpret_cast<char *>(lds) + G::kXchgBytes +
                   rw * (kRowsPerWave * kRowBytes);
