@@ -136,12 +136,14 @@ def build_extension() -> str:
 _M0_IMPLICIT_READERS = ("s_movrel", "v_movrel", "s_sendmsg", "ds_gws", "ds_append",
                         "ds_consume", "v_interp", "ds_read_addtid", "ds_write_addtid",
                         "s_ttracedata", "buffer_load_lds")
-_M0_WRITE = re.compile(r"s_mov_b32 m0, s\d+$")
+# The m0 value is an "s" operand of the asm, so the allocator may place it in
+# any SGPR, VCC's halves included.
+_M0_WRITE = re.compile(r"s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$")
 
 
 def m0_problems(asm: str) -> list:
     """Every instruction in `asm` (AMDGPU assembly) that defines or reads m0
-    other than the global_to_lds16 pattern `s_mov_b32 m0, sN` [s_nop ...]
+    other than the global_to_lds16 pattern `s_mov_b32 m0, <SGPR>` [s_nop ...]
     `global_load_lds_dwordx4`, and every global_load_lds without that write
     right before it."""
     code = []

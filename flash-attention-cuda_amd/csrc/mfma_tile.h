@@ -71,7 +71,39 @@ __device__ __forceinline__ void global_to_lds16_sbase(const void *base, unsigned
       : "v"(voff), "s"(base), "s"(m0)
       : "memory", "m0");
 }
+// The same two loads with the LDS destination given as a byte address (a
+// wave-uniform value kept from lds_addr): no generic-to-LDS pointer cast, and
+// so no null check, per load.
+__device__ __forceinline__ void global_to_lds16_at(const void *src, unsigned lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_dst);
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(m0)
+      : "memory", "m0");
+}
+__device__ __forceinline__ void global_to_lds16_sbase_at(const void *base, unsigned voff,
+                                                         unsigned lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_dst);
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
 #pragma clang diagnostic pop
+
+// LDS byte address of a pointer into a __shared__ array. The generic-to-LDS
+// cast carries a null check; callers take it once and do their address
+// arithmetic on the integer.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
+}
 
 // Wait until at most N of this thread's global->LDS loads are outstanding.
 template <int N>
@@ -202,6 +234,12 @@ __device__ __forceinline__ lds_half *opaque_lds(const _Float16 *p) {
 __device__ __forceinline__ unsigned uniform_lds_base(const _Float16 *p) {
   unsigned a = __builtin_amdgcn_readfirstlane(
       static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_half *)(p))));
+  asm volatile("" : "+s"(a));
+  return a;
+}
+// uniform_lds_base for a tile already given as an LDS byte address.
+__device__ __forceinline__ unsigned uniform_lds_u(unsigned a) {
+  a = __builtin_amdgcn_readfirstlane(a);
   asm volatile("" : "+s"(a));
   return a;
 }

@@ -207,9 +207,8 @@ struct VFrags { half8 f[Geo<D>::kKS][Geo<D>::kDB]; };  // [16-key step][d-block]
 
 
 template <int D>
-__device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
-                                       const FragOffsetsD<D> &fo, KFrags<D> &k) {
-  const unsigned base = uniform_lds_base(tile);
+__device__ __forceinline__ void read_k(unsigned tile, const FragOffsetsD<D> &fo, KFrags<D> &k) {
+  const unsigned base = uniform_lds_u(tile);
 #pragma unroll
   for (int s = 0; s < Geo<D>::kDS; ++s) {
     lds_half *p = opaque_lds_at(base, fo.k[s]);
@@ -221,9 +220,8 @@ __device__ __forceinline__ void read_k(const _Float16 *__restrict__ tile,
 }
 
 template <int D>
-__device__ __forceinline__ void read_v(const _Float16 *__restrict__ tile,
-                                       const FragOffsetsD<D> &fo, VFrags<D> &v) {
-  const unsigned base = uniform_lds_base(tile);
+__device__ __forceinline__ void read_v(unsigned tile, const FragOffsetsD<D> &fo, VFrags<D> &v) {
+  const unsigned base = uniform_lds_u(tile);
 #pragma unroll
   for (int db = 0; db < Geo<D>::kDB; ++db) {
     lds_half *p = opaque_lds_at(base, fo.v[db]);
@@ -444,7 +442,7 @@ __device__ __forceinline__ void slow_step(const KFrags<D> &kf, const VFrags<D> &
 template <int D>
 struct HalfRing {
   using G = Geo<D>;
-  _Float16 *kring, *vring;
+  unsigned kring, vring;  // LDS byte addresses of the two rings
   const _Float16 *kp, *vp;
   int seq, n_tiles, half;
   unsigned voff[2][2];  // [K|V][row block i]: byte offset of this lane's chunk in a tile
@@ -453,11 +451,11 @@ struct HalfRing {
 
   __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
   __device__ __forceinline__ bool exists(int k) const { return tile(k) < n_tiles; }
-  __device__ __forceinline__ _Float16 *kstage(int k) const {
-    return kring + (k % kKStages) * G::kTileHalves;
+  __device__ __forceinline__ unsigned kstage(int k) const {
+    return kring + (k % kKStages) * (2 * G::kTileHalves);
   }
-  __device__ __forceinline__ _Float16 *vstage(int k) const {
-    return vring + (k % kVStages) * G::kTileHalves;
+  __device__ __forceinline__ unsigned vstage(int k) const {
+    return vring + (k % kVStages) * (2 * G::kTileHalves);
   }
   // The half's four waves each load row blocks {2 wh, 2 wh + 1} (one wave
   // load each: 8 rows of 128 B for D = 64, 4 rows of 256 B for D = 128) of K
@@ -467,8 +465,8 @@ struct HalfRing {
   __device__ __forceinline__ void issue(int k) const {
     if (!exists(k)) return;
     const int key0 = tile(k) * G::kBc;
-    _Float16 *const ks = kstage(k);
-    _Float16 *const vs = vstage(k);
+    const unsigned ks = kstage(k);
+    const unsigned vs = vstage(k);
     if (key0 + G::kBc <= seq) {
       // Whole tile inside the sequence: a scalar tile base plus the lane's
       // fixed offset.
@@ -476,16 +474,16 @@ struct HalfRing {
       const _Float16 *const vb = vp + static_cast<size_t>(key0) * D;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        global_to_lds16_sbase(kb, voff[0][i], ks + lds_off[i]);
-        global_to_lds16_sbase(vb, voff[1][i], vs + lds_off[i]);
+        global_to_lds16_sbase_at(kb, voff[0][i], ks + 2 * lds_off[i]);
+        global_to_lds16_sbase_at(vb, voff[1][i], vs + 2 * lds_off[i]);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int in_row = row_in_tile[i] * D;
         const size_t row = static_cast<size_t>(min(key0 + row_in_tile[i], seq - 1)) * D;
-        global_to_lds16(kp + row + (voff[0][i] / 2 - in_row), ks + lds_off[i]);
-        global_to_lds16(vp + row + (voff[1][i] / 2 - in_row), vs + lds_off[i]);
+        global_to_lds16_at(kp + row + (voff[0][i] / 2 - in_row), ks + 2 * lds_off[i]);
+        global_to_lds16_at(vp + row + (voff[1][i] / 2 - in_row), vs + 2 * lds_off[i]);
       }
     }
   }
@@ -577,8 +575,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   _Float16 *const half_lds = lds + G::kQHalves + half * G::kHalfHalves;
   _Float16 *const q_lds = lds;
   HalfRing<D> ring;
-  ring.kring = half_lds;
-  ring.vring = half_lds + kKStages * G::kTileHalves;
+  ring.kring = lds_addr(half_lds);
+  ring.vring = ring.kring + kKStages * (2 * G::kTileHalves);
   ring.seq = seq;
   ring.half = half;
 #pragma unroll
