@@ -28,6 +28,9 @@ prefill_kernel:
 \ts_mov_b32 m0, s5
 \ts_nop 0
 \tglobal_load_lds_dwordx4 v[4:5], off
+\ts_mov_b32 m0, vcc_lo
+\ts_nop 0
+\tglobal_load_lds_dwordx4 v6, s[8:9]
 """
 
 
@@ -41,6 +44,7 @@ def test_m0_checker_accepts_the_load_sequence():
     "\ts_sendmsg sendmsg(MSG_INTERRUPT)\n",               # implicit m0 read
     "\ts_mov_b32 s7, m0\n",                               # m0 read
     "\tglobal_load_lds_dwordx4 v1, off\n",                # load without its m0 write
+    "\ts_mov_b32 m0, v0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 v1, off\n",  # not an SGPR
     "\ts_mov_b32 m0, s4\n\tv_add_u32_e32 v1, v2, v3\n\tglobal_load_lds_dwordx4 v1, off\n",
 ])
 def test_m0_checker_flags_other_uses(planted):
