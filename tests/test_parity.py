@@ -274,6 +274,46 @@ def test_peaky_rows_in_some_query_tiles_only(causal):
     _check(out16, out32, ref, f"rows 600-699 x3 causal={causal}")
 
 
+@pytest.mark.parametrize("seq", [1023, 1024, 1025, 1280])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("width", [1.0, 3.4 ** 0.5])
+def test_lazy_max_boundary(seq, causal, width):
+    """Rows that see >= 1024 keys take the lazy max at head_dim 64 (m moves
+    only when a tile max exceeds it by more than 2^8), shorter rows keep the
+    exact running max. Lengths on both sides of that boundary, at the N(0,1)
+    width and a wider one whose peaky rows the rounded-mass check must catch,
+    all within the bound."""
+    q, k, v = oracle.make_prefill_inputs(1, 2, seq, seed=61)
+    q = (q.float() * width).half()
+    k = (k.float() * width).half()
+    ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    out32 = flashattn_cuda._prefill_fp32(q.cuda(), k.cuda(), v.cuda(), causal, SCALE)
+    out16 = flashattn_cuda.prefill(q.cuda(), k.cuda(), v.cuda(), causal, SCALE)
+    _check(out16, out32, ref, f"S={seq} causal={causal} width {width:.2f}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_lazy_max_late_rise_and_slow_drift(causal):
+    """Two ways the running max moves on long rows. Head 0: keys 1500-1519
+    scaled x4, so the maxima of rows that reach them jump far above the
+    earlier tiles' (m moves on that tile and O is rescaled). Head 1: logits
+    that grow steadily along the sequence (by ~7.8 in log2 units over 2048
+    keys), so under the lazy max m stays where the first tile put it and P
+    climbs towards 2^8 without a rescale. Both against the oracle."""
+    seq = 2048
+    q, k, v = oracle.make_prefill_inputs(1, 2, seq, seed=67)
+    q, k = q.float(), k.float()
+    k[:, 0, 1500:1520] *= 4.0
+    q[:, 1] = 0.0
+    q[:, 1, :, 0] = 8.0
+    k[:, 1, :, 0] = torch.arange(seq, dtype=torch.float32) / seq * 5.4
+    q, k = q.half(), k.half()
+    ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    out32 = flashattn_cuda._prefill_fp32(q.cuda(), k.cuda(), v.cuda(), causal, SCALE)
+    out16 = flashattn_cuda.prefill(q.cuda(), k.cuda(), v.cuda(), causal, SCALE)
+    _check(out16, out32, ref, f"late rise / slow drift causal={causal}")
+
+
 def test_decode_equals_prefill_rows_at_full_size():
     """Every position t of a long causal prefill equals decode at len t+1."""
     q, k, v = oracle.make_prefill_inputs(2, 14, 4096, seed=10)
