@@ -43,8 +43,8 @@
 // Main loop (tiles that need no mask), per wave and step k of its half:
 //   wait for tile k+2 and this wave's LDS reads -> barrier -> issue the loads
 //   of tile k+4 ->
-//   charge the rounded mass of P_{k-2} -> O *= alpha_{k-1} (only when m
-//   moved) -> row max of S_k ->
+//   note the row sum (head_dim 64) -> O *= alpha_{k-1} (only when m moved) ->
+//   row max of S_k ->
 //   { QK(k+1), PV(k-1) and the row sums of P_{k-1} on the matrix cores }
 //   interleaved with { exp / pack of S_k on the VALU } ->
 //   LDS reads of the next step's fragments (K_{k+2}, V_k), which land while
@@ -81,29 +81,29 @@
 // head_dim 64 on the matrix cores (one v_mfma_f32_16x16x32_f16 per 16-key
 // step against a 0/1 selector, rowsum_mfma), at head_dim 128 per lane with
 // v_dot2_f32_f16.
-// The max m: rows that see >= 1024 keys (head_dim 64) take a lazy max. m
-// moves, to the row's exact running max, only when a tile max exceeds it by
-// more than 8 (log2 units), so P <= 2^8 and O is rescaled on a few steps per
-// item instead of on most of them. Shorter rows, and every row at head_dim
-// 128, keep m at the exact running max (every step where some row's max rose
-// rescales). Whenever a tile sets m, its dominant key enters the PV product
-// as P = 1 exactly.
+// The max m: rows that see >= 1024 keys take a lazy max. m moves, to the
+// row's exact running max, only when a tile max exceeds it by more than 8
+// (log2 units), so P <= 2^8, or when the new max carries more than 1/16 of
+// the row sum so far; O is then rescaled on a few steps per item instead of
+// on most of them. Shorter rows keep m at the exact running max (every step
+// where some row's max rose rescales). Whenever a tile sets m, its dominant
+// key enters the PV product as P = 1 exactly.
 //
 // Precision of P: one fp16 rounding of each weight w = p / l moves an output
 // row by about 2^-11 sqrt(sum w^2) times the spread of V, summed over the
 // rounded weights (a P = 1 key is exact and does not count). Rows carried by
 // a few keys therefore need P split into hi + lo fp16 parts, with the PV
 // product issued twice (relative error ~2^-22). Rows that see fewer than 256
-// keys always take the split. Every other row tracks an upper bound of its
-// rounded mass r = sum w^2: per tile, (largest weight) x (weight sum), minus
-// the exact 1 of a tile whose largest weight is exactly 1, rescaled with m
-// like l. (head_dim 64 takes a tile's weight sum from the row-sum
-// accumulator two steps later, charge_mass.) A block with a row whose
-// r / l^2 ends above kRedoRoundedMassAbove (0.08: output error ~2e-4 at the
-// bound, measured on inputs up to 3.4x the N(0,1) logit width) is computed
-// again with split P on every tile. Independent N(0,1) inputs at 1/sqrt(D)
-// stay below 0.065 (rows with 256-383 keys) and below 0.045 beyond, so they
-// take the single-rounding pass only.
+// keys always take the split. Every other row sums its rounded mass
+// r = sum P^2 over the fp16 weights it rounded (v_dot2_f32_f16 of the packed
+// P with itself), less the exact 1 of a tile whose largest weight is exactly
+// 1, rescaled with m like l. A block with a row whose r / l^2 ends above
+// kRedoRoundedMassAbove is computed again with split P on every tile.
+// Measured on N(0,1) q, k, v scaled to 1x-1.84x the standard logit width
+// (head_dim 64 and 128, causal and full, 512-2048 keys): rows kept at
+// r / l^2 <= 0.03 show fp32-output errors <= 2.17e-4 (error up to ~1.5e-3 x
+// sqrt(r / l^2)); N(0,1) inputs at 1/sqrt(D) stay below 0.013 and take the
+// single-rounding pass only.
 
 #include <algorithm>
 #include <type_traits>
@@ -126,16 +126,19 @@ constexpr int kLoadsPerTile = 4;              // global_load_lds per thread per 
 constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split P
 // A block is recomputed with split P when, for one of its rows, the squared
 // normalised weights that took a single fp16 rounding sum to more than this
-// (bounded per tile by the tile's largest weight times its weight sum; see the
-// precision note at the top of the file).
-constexpr float kRedoRoundedMassAbove = 0.08f;
+// (see the precision note at the top of the file).
+constexpr float kRedoRoundedMassAbove = 0.03f;
 // |scale| * sqrt(D) above this (1 is the standard 1/sqrt(D)): rows are peaky
 // from the scale alone, so the first (single-rounding) pass is skipped.
 constexpr float kSplitAllWidth = 1.5f;
 constexpr float kNegHuge = -3.0e38f;
 // The max that P is taken against moves only when a row's tile max exceeds it
-// by more than this (log2 units), so P <= 2^8 and O is rescaled on few steps.
+// by more than this (log2 units), so P <= 2^8 and O is rescaled on few steps...
 constexpr float kLazyMaxSlack = 8.0f;
+// ...or when the tile max's weight exceeds this fraction of the row sum so
+// far: a key that carries a large share of its row is then taken at the exact
+// max, where its P = 1 is exact and leaves the rounded mass.
+constexpr float kLazyMaxDominant = 1.0f / 16;
 constexpr int kLazyMaxRowsFrom = 1024;  // keys a row sees (at least) to take the lazy max
 
 // Tile geometry for head_dim D (64 or 128). A K or V tile is always 8 KiB:
@@ -179,21 +182,21 @@ __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
   return *reinterpret_cast<const half8 *>(p);
 }
 
-// head_dim 64 sums P rows on the matrix cores (rowsum_mfma) and takes the
-// lazy max on long rows; head_dim 128, whose loop has no registers to spare,
-// sums them with v_dot2_f32_f16 per lane and keeps the exact running max.
+// head_dim 64 sums P rows on the matrix cores (rowsum_mfma); head_dim 128,
+// whose loop has no registers to spare, sums them with v_dot2_f32_f16 per
+// lane.
 template <int D>
 constexpr bool kMfmaRowSum = D == 64;
 
-// Per-lane softmax state of one query row. head_dim 64: both lanes of a pair
-// hold the same m, mt, r and row sum (lacc[0]). head_dim 128: m is the exact
-// running max, l and r are this lane's shares of the row's sums.
+// Per-lane softmax state of one query row. Both lanes of a pair hold the same
+// m and mt; r is this lane's share of the row's rounded mass; head_dim 64:
+// both lanes hold the row sum (lacc[0]); head_dim 128: l is this lane's share.
 template <int D>
 struct SoftmaxState {
   float m;                      // the max P is taken against (log2 domain, scaled by c)
   float mt;                     // the row's true running max (log2 domain)
-  float r;                      // rounded-mass bound (below), in units of m
-  float lprev;                  // row sum already charged to r (head_dim 64)
+  float r;                      // rounded mass: sum of P^2 of rounded weights, units of m
+  float lprev;                  // row sum at the start of the step (head_dim 64)
   float l;                      // this lane's share of the row sum (head_dim 128)
   floatx4 lacc;                 // row sum on the matrix cores: element 0 (head_dim 64)
   floatx16 o[Geo<D>::kDB];      // O^T accumulators, one per 32-dim block
@@ -278,9 +281,12 @@ __device__ __forceinline__ void rowsum_mfma(const half8 &sel, const half8 (&p)[G
 
 // Row max of one tile and the lazy update of m. Returns whether the wave
 // rescales (wave-uniform): m moves, to the row's exact running max, only when
-// some row of the wave has a tile max more than kLazyMaxSlack above its m;
-// alpha (set then) rescales the previous O, row sum and rounded mass. pm is
-// the tile's largest weight in units of the (new) m.
+// some row of the wave has a tile max more than kLazyMaxSlack above its m, or
+// one whose weight exceeds kLazyMaxDominant times the row sum so far (head_dim
+// 64: lprev, the sum at the start of the step; head_dim 128: the lane's share
+// l); alpha (set then) rescales the previous O and row sum (head_dim 64: at
+// the next step's rescale_o) and the rounded mass. pm is the tile's largest
+// weight in units of the (new) m.
 // MASK: keys past the end or above the causal diagonal become -inf.
 template <bool CAUSAL, bool MASK, int D>
 __device__ __forceinline__ bool tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, float c_scale,
@@ -305,32 +311,33 @@ __device__ __forceinline__ bool tile_max(floatx16 (&s)[Geo<D>::kKB], int lim, fl
     mx_c = mx * c_scale;
   }
   st.mt = fmaxf(st.mt, mx_c);
-  const bool rescale = __builtin_amdgcn_ballot_w64(mx_c > st.m + slack) != 0;
+  pm = fast_exp2(mx_c - st.m);
+  const float l_seen = kMfmaRowSum<D> ? st.lprev : st.l;
+  const bool move = mx_c > st.m + slack || pm > fmaxf(1.0f, kLazyMaxDominant * l_seen);
+  const bool rescale = __builtin_amdgcn_ballot_w64(move) != 0;
   alpha = 1.0f;
   if (rescale) {
     alpha = fast_exp2(st.m - st.mt);
     st.m = st.mt;
-    if constexpr (!kMfmaRowSum<D>) {
-      st.l *= alpha;
-      st.r *= alpha * alpha;
-    }
+    if constexpr (!kMfmaRowSum<D>) st.l *= alpha;
+    st.r *= alpha * alpha;
+    pm = fast_exp2(mx_c - st.m);
   }
-  pm = fast_exp2(mx_c - st.m);
   return rescale;
 }
 
 // P^T fragments (hi [+ lo]) of one tile. head_dim 128 also adds the tile to
-// its row-sum share and, with one rounding of P, its rounded mass: the tile's
-// largest weight pm times its weight sum, minus the exact 1 of a tile whose
-// largest weight is the running max (half of it in each lane of the pair,
-// since only their sum is used).
+// its row-sum share. With one rounding of P, the lane adds the squares of its
+// rounded weights to its share of the rounded mass, less the exact 1 of a
+// tile whose largest weight is exactly 1 (the key at m: fp16 holds it
+// exactly; half of it in each lane of the pair, since only their sum is used).
 template <bool MASK, bool SPLIT, int D>
 __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float c_scale,
                                          float pm, SoftmaxState<D> &st,
                                          half8 (&p_hi)[Geo<D>::kKS],
                                          half8 (&p_lo)[Geo<D>::kKS]) {
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-  float lsum = 0.f;
+  float lsum = 0.f, sq = 0.f;
   const float m_use = st.m;
 #pragma unroll
   for (int ks = 0; ks < Geo<D>::kKS; ++ks) {
@@ -348,6 +355,7 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float
       p_hi[ks][t] = hi2[0];
       p_hi[ks][t + 1] = hi2[1];
       if constexpr (!kMfmaRowSum<D>) lsum = __builtin_amdgcn_fdot2(hi2, ones, lsum, false);
+      if (!SPLIT) sq = __builtin_amdgcn_fdot2(hi2, hi2, sq, false);
       if (SPLIT) {
         const half2 lo2 = {static_cast<_Float16>(p0 - static_cast<float>(hi2[0])),
                            static_cast<_Float16>(p1 - static_cast<float>(hi2[1]))};
@@ -357,13 +365,12 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float
       }
     }
   }
-  if constexpr (!kMfmaRowSum<D>) {
-    st.l += lsum;
-    if (!SPLIT) st.r = fmaf(-0.5f, floorf(pm), fmaf(pm, lsum, st.r));
-  }
+  if constexpr (!kMfmaRowSum<D>) st.l += lsum;
+  if (!SPLIT) st.r += sq - (pm == 1.0f ? 0.5f : 0.0f);
 }
 
-// O, the row sum and the rounded mass follow a move of m (wave-uniform branch).
+// O (and, head_dim 64, the row sum on the matrix cores) follow a move of m
+// (wave-uniform branch).
 template <int D>
 __device__ __forceinline__ void rescale_o(SoftmaxState<D> &st, float alpha, bool rescale) {
   if (rescale) {
@@ -374,21 +381,15 @@ __device__ __forceinline__ void rescale_o(SoftmaxState<D> &st, float alpha, bool
     if constexpr (kMfmaRowSum<D>) {
       st.lacc[0] *= alpha;
       st.lprev *= alpha;
-      st.r *= alpha * alpha;
     }
   }
 }
 
-// Rounded mass: the row-sum growth since the last charge, times an upper bound
-// of the largest weight among the tiles it came from (a pm taken before a
-// later move of m only overstates it), is an upper bound of those tiles'
-// squared weights.
+// head_dim 64: the row sum the next tile_max weighs a new max against (the
+// accumulator as the step starts, which holds P up to two steps back).
 template <int D>
-__device__ __forceinline__ void charge_mass(SoftmaxState<D> &st, float pm) {
-  if constexpr (!kMfmaRowSum<D>) return;
-  const float l_now = st.lacc[0];
-  st.r = fmaf(pm, l_now - st.lprev, st.r) - (pm == 1.0f ? 1.0f : 0.0f);
-  st.lprev = l_now;
+__device__ __forceinline__ void note_row_sum(SoftmaxState<D> &st) {
+  if constexpr (kMfmaRowSum<D>) st.lprev = st.lacc[0];
 }
 
 // Scheduling pipeline for one main step: each of its MFMAs followed by a
@@ -408,10 +409,13 @@ __device__ __forceinline__ void interleave_step() {
 // Pins the P fragments of a step to that step: without a use there, the
 // compiler sinks their computation into the next step (next to the PV MFMAs
 // that consume them), which defeats the interleave.
-template <int N>
-__device__ __forceinline__ void keep(const half8 (&p)[N]) {
+// The rounded mass gets the same pin: its squares would otherwise sink to the
+// next step's row max, outside the interleave.
+template <int N, int D>
+__device__ __forceinline__ void keep(const half8 (&p)[N], const SoftmaxState<D> &st) {
 #pragma unroll
   for (int ks = 0; ks < N; ++ks) asm volatile("" ::"v"(p[ks]));
+  asm volatile("" ::"v"(st.r));
 }
 
 // Plain (non-pipelined) step for masked / short-row tiles: QK, softmax with
@@ -645,7 +649,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // Rows that see many keys take the lazy max; shorter ones keep m at the
   // exact running max, whose P = 1 key takes no rounding.
   const float slack =
-      kMfmaRowSum<D> && (CAUSAL ? q0 : seq) >= kLazyMaxRowsFrom ? kLazyMaxSlack : 0.f;
+      (CAUSAL ? q0 : seq) >= kLazyMaxRowsFrom ? kLazyMaxSlack : 0.f;
 
   half8 qf[kDS];
   SoftmaxState<D> st;
@@ -773,10 +777,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     KFrags<D> kf;
     VFrags<D> vf;
     // alpha / rescale: the move of m that the next step applies to O before
-    // its PV. pm_a, pm_b: largest weights of the P tiles in p_a, p_b, kept
-    // until their row sums are charged to the rounded mass (charge_mass at the
-    // start of the step after the one that issued their row-sum MFMAs).
-    float alpha, pm_a, pm_b = 0.f;
+    // its PV. pm_a, pm_b: largest weights of the P tiles in p_a, p_b.
+    float alpha, pm_a, pm_b;
     bool rescale;
     read_k(ring.kstage(0), fo, kf);
     qk_mfma(kf, qf, s_a);
@@ -793,11 +795,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     kk = 1;
 
     // steps kk (odd: S_kk in s_b, P_{kk-1} in p_a) and kk + 1 (even); kf and
-    // vf hold K_{kk+1} and V_{kk-1}. At step k the row-sum accumulator holds
-    // P up to k - 2, so charge_mass charges P_{k-2} (pm of the same parity).
+    // vf hold K_{kk+1} and V_{kk-1}.
     for (; kk + 1 < n_main; kk += 2) {
       ring.advance(kk);
-      charge_mass(st, pm_b);
+      note_row_sum(st);
       rescale_o(st, alpha, rescale);
       rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
       rowsum_mfma<D>(sel, p_a, st.lacc);
@@ -805,12 +806,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       pv_mfma(vf, p_a, st.o);
       tile_exp<false, false>(s_b, c_scale, pm_b, st, p_b, p_unused);
       interleave_step<D>();
-      keep(p_b);
+      keep(p_b, st);
       read_k(ring.kstage(kk + 2), fo, kf);
       read_v(ring.vstage(kk), fo, vf);
 
       ring.advance(kk + 1);
-      charge_mass(st, pm_a);
+      note_row_sum(st);
       rescale_o(st, alpha, rescale);
       rescale = tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
       rowsum_mfma<D>(sel, p_b, st.lacc);
@@ -818,7 +819,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       pv_mfma(vf, p_b, st.o);
       tile_exp<false, false>(s_a, c_scale, pm_a, st, p_a, p_unused);
       interleave_step<D>();
-      keep(p_a);
+      keep(p_a, st);
       read_k(ring.kstage(kk + 3), fo, kf);
       read_v(ring.vstage(kk + 1), fo, vf);
     }
@@ -830,12 +831,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // (head_dim 128: its 32-key tiles put two masked tiles in each half's
     // range; the second one takes the plain step below.)
     const bool tail = n_steps >= n_main + 1;
-    // Largest weights of the two P tiles not yet charged: the one whose row
-    // sums the last step issued, and the one still waiting for its PV.
-    float pm_summed = pm_b, pm_pending = pm_a;
     if (kk < n_main) {  // one more (odd) main step; leaves S_{kk+1} in s_b, P_kk in p_a
       ring.advance(kk);
-      charge_mass(st, pm_b);
+      note_row_sum(st);
       rescale_o(st, alpha, rescale);
       rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
       if (tail) qk_mfma(kf, qf, s_a);
@@ -846,12 +844,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       ++kk;
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) s_b[kb] = s_a[kb];
-      pm_summed = pm_a;
-      pm_pending = pm_b;
     }
-    // The last tiles are charged one at a time (each charge waits for the
-    // row-sum MFMAs before it, once per item).
-    charge_mass(st, pm_summed);
     if (tail) {
       ring.advance(kk);
       const int key0 = ring.tile(kk) * kBc;
@@ -859,7 +852,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       rescale_o(st, alpha, rescale);
       rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
-      charge_mass(st, pm_pending);
       if (active) {
         const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
         float pm_t;
@@ -869,14 +861,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
         rescale_o(st, alpha, rescale);
         rowsum_mfma<D>(sel, p_a, st.lacc);
         pv_mfma(vf, p_a, st.o);
-        charge_mass(st, pm_t);
       }
       ++kk;
     } else {
       rescale_o(st, alpha, rescale);
       rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
-      charge_mass(st, pm_pending);
     }
   }
 
@@ -892,7 +882,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // barrier every wave reads all four.
     if (half == 0) {
       const float l_row = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
-      const float r_row = kMfmaRowSum<D> ? st.r : st.r + __shfl_xor(st.r, 32);
+      const float r_row = st.r + __shfl_xor(st.r, 32);
       const bool peaky = my_q < seq && r_row > kRedoRoundedMassAbove * l_row * l_row;
       const float verdict = __builtin_amdgcn_ballot_w64(peaky) != 0 ? 1.0f : 0.0f;
       if (lane == 0) xchg[0] = verdict;
