@@ -220,7 +220,7 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float acc[8],
 // the code object loads and are split into slots, one per (device, stream)
 // in use, so calls that may overlap in time (other streams) never share one.
 constexpr int kCounterSlots = 64;
-constexpr int kCountersPerSlot = 4096;
+constexpr int kCountersPerSlot = static_cast<int>(kMergeCountersPerSlot);
 __device__ unsigned g_merge_counters[kCounterSlots * kCountersPerSlot];
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -232,17 +232,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
   return x;
-}
-
-// Partials that another wave of the same launch reads: relaxed agent-scope
-// atomic stores and loads, which go to the device-coherent level (sc1) on
-// their own, so the only ordering needed is the writer's wait for its stores
-// before it counts (no cache-wide release or acquire).
-__device__ __forceinline__ void store_coherent(float *p, float x) {
-  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One wave merges the n_act partials of one (b, h) (slots base .. base +
@@ -1064,9 +1053,23 @@ bool use_bh_path(int batch, int heads, int max_seq) {
   return cu > 0 && (static_cast<long long>(batch) * heads >= cu || max_seq <= kBhShortCache);
 }
 
+// Queries per wave of the grouped pass: the largest divisor of the group
+// that fits the 32 columns of one MFMA tile.
+int group_queries(int group) {
+  for (int nq = min(group, kGroupCols); nq > 1; --nq)
+    if (group % nq == 0) return nq;
+  return 1;
+}
+
+
+
+}  // namespace
+
 // Counter slot of g_merge_counters for the current device and `stream`,
-// claimed on first use and kept; nullptr (the two-launch path) when the
-// (b, h) count exceeds a slot or every slot is taken.
+// claimed on first use and kept; nullptr (decode: the two-launch path) when
+// n_bh counters exceed a slot or every slot is taken. The split-K decode and
+// the split prefill units share a stream's slot: kernels on one stream run
+// one at a time, and each leaves its counters at zero.
 unsigned *merge_counters(hipStream_t stream, size_t n_bh) {
   if (n_bh > static_cast<size_t>(kCountersPerSlot)) return nullptr;
   int dev = 0;
@@ -1095,18 +1098,6 @@ unsigned *merge_counters(hipStream_t stream, size_t n_bh) {
   owner[n_used] = {dev, stream};
   return base[dev] + static_cast<size_t>(n_used++) * kCountersPerSlot;
 }
-
-// Queries per wave of the grouped pass: the largest divisor of the group
-// that fits the 32 columns of one MFMA tile.
-int group_queries(int group) {
-  for (int nq = min(group, kGroupCols); nq > 1; --nq)
-    if (group % nq == 0) return nq;
-  return 1;
-}
-
-
-
-}  // namespace
 
 bool decode_needs_workspace(int batch, int heads, int kv_heads, int max_seq) {
   return heads != kv_heads || !use_bh_path(batch, heads, max_seq);

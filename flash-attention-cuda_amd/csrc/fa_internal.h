@@ -40,9 +40,15 @@ int device_cu_count(int device);
 // ---- kernel launchers (prefill.hip / decode.hip) ---------------------------
 // kv_heads divides heads; query head h reads K/V head h / (heads / kv_heads).
 // head_dim is 64 or 128.
+// workspace (may be NULL): prefill_workspace_bytes(...) bytes let the launch
+// split the heaviest items' key ranges over more CUs (with less, it does not).
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
                    bool out_f32, int batch, int heads, int kv_heads, int seq,
-                   int head_dim, bool causal, float scale, hipStream_t stream);
+                   int head_dim, bool causal, float scale, void *workspace,
+                   size_t workspace_bytes, hipStream_t stream);
+// Workspace that lets launch_prefill split items for this shape on the
+// current device (either head size), 0 when it would not split.
+size_t prefill_workspace_bytes(int batch, int heads, int seq, bool causal);
 // head_dim is 64 or 128; grouped queries take the matrix-core grouped pass
 // and the merge, the others the VALU split-K / whole-sequence kernels.
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,
@@ -53,6 +59,12 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
 // shape on the current device: the whole-sequence kernel (no grouped queries,
 // B * H >= CUs or a short cache) merges in LDS and needs none.
 bool decode_needs_workspace(int batch, int heads, int kv_heads, int max_seq);
+// Counter slot (kMergeCountersPerSlot zeroed counters) of the current device
+// for kernels launched on `stream`, claimed on first use and kept; nullptr
+// when `n` counters exceed a slot or every slot is taken. Kernels that count
+// arrivals in it set each counter back to zero before they end (decode.hip).
+constexpr size_t kMergeCountersPerSlot = 4096;
+unsigned *merge_counters(hipStream_t stream, size_t n);
 // Decode work units per batch row: one per head without grouped queries,
 // else one per (K/V head, chunk of up to 32 of its query heads).
 int decode_units_per_row(int heads, int kv_heads);

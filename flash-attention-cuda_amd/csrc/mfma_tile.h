@@ -266,5 +266,17 @@ __device__ __forceinline__ float max_lane_pair(float x) {
   return a;
 }
 
+
+// Partials that another wave of the same launch reads: relaxed agent-scope
+// atomic stores and loads, which go to the device-coherent level (sc1) on
+// their own, so the only ordering needed is the writer's wait for its stores
+// before it counts (no cache-wide release or acquire).
+__device__ __forceinline__ void store_coherent(float *p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 }  // namespace fa

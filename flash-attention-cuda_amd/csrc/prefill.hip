@@ -106,7 +106,11 @@
 // single-rounding pass only.
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
+#include <vector>
 
 #include "fa_internal.h"
 #include "mfma_tile.h"
@@ -448,12 +452,12 @@ struct HalfRing {
   using G = Geo<D>;
   unsigned kring, vring;  // LDS byte addresses of the two rings
   const _Float16 *kp, *vp;
-  int seq, n_tiles, half;
+  int seq, t0, n_tiles, half;  // this half streams tiles t0 + 2 k + half below n_tiles
   unsigned voff[2][2];  // [K|V][row block i]: byte offset of this lane's chunk in a tile
   int row_in_tile[2];
   int lds_off[2];       // row block i of this wave, in halves
 
-  __device__ __forceinline__ int tile(int k) const { return 2 * k + half; }
+  __device__ __forceinline__ int tile(int k) const { return t0 + 2 * k + half; }
   __device__ __forceinline__ bool exists(int k) const { return tile(k) < n_tiles; }
   __device__ __forceinline__ unsigned kstage(int k) const {
     return kring + (k % kKStages) * (2 * G::kTileHalves);
@@ -518,7 +522,7 @@ struct HalfRing {
 // within a level each XCD fills its positions with its home heads first and
 // the leftover heads take the spare positions in a fixed order, so most of a
 // head's blocks share one XCD's L2 (for 14 heads, 89 % of the blocks).
-__device__ __forceinline__ int home_head(int i, int n_bh) {
+__host__ __device__ __forceinline__ int home_head(int i, int n_bh) {
   const int level = i / n_bh;
   const int k = i - level * n_bh;
   const int base = (level * n_bh) & 7;
@@ -533,12 +537,12 @@ __device__ __forceinline__ int home_head(int i, int n_bh) {
   for (int y = 0; y < x; ++y) {
     const int npos = (n_bh - ((y - base) & 7) + 7) >> 3;
     const int nhome = (n_bh - y + 7) >> 3;
-    s += max(0, npos - nhome);
+    s += npos > nhome ? npos - nhome : 0;
   }
   for (int y = 0; y < 8; ++y) {
     const int npos = (n_bh - ((y - base) & 7) + 7) >> 3;
     const int nhome = (n_bh - y + 7) >> 3;
-    const int over = max(0, nhome - npos);
+    const int over = nhome > npos ? nhome - npos : 0;
     if (s < over) return y + 8 * (npos + s);
     s -= over;
   }
@@ -549,18 +553,41 @@ __device__ __forceinline__ int home_head(int i, int n_bh) {
 // given a contiguous run of query heads, in XCD order, so the query heads
 // that read one K/V head (consecutive indices) mostly share an XCD and its
 // L2 holds one copy of that K/V head.
-__device__ __forceinline__ int grouped_head(int h, int n_bh) {
+__host__ __device__ __forceinline__ int grouped_head(int h, int n_bh) {
   const int x = h & 7;
   int start = 0;
   for (int y = 0; y < x; ++y) start += (n_bh - y + 7) >> 3;
   return start + (h >> 3);
 }
 
+// Work units and their blocks, planned on the host when the items do not
+// fill the chip evenly (at most two per CU): the heaviest items are split
+// into two key chunks, tiles [0, mid) and [mid, n_tiles) with mid =
+// split_mid(n_tiles), and every block takes (up to) two units, heavy with
+// light. A unit is pos | code << 20 | split << 22: item pos (numbered as in
+// the kernel), code 0 for the whole key range, 1 / 2 for the first / second
+// chunk, split = the item's index among the split items (its partial slots
+// and counters). n_blocks = 0: no plan, blocks take items by formula.
+constexpr int kPlanMaxBlocks = 384;
+constexpr unsigned kNoUnit = 0xffffffffu;
+struct PrefillPlan {
+  int n_blocks;
+  unsigned unit[2 * kPlanMaxBlocks];  // block b: unit[2 b] first, unit[2 b + 1] second
+};
+__host__ __device__ __forceinline__ int split_mid(int n_tiles) { return (n_tiles / 2) & ~1; }
+// Partial of one row wave of one chunk: O^T accumulators (lane-major), then m
+// and the row sum (or head_dim 128's per-lane share of it), one per lane.
+template <int D>
+constexpr int kPartOFloats = Geo<D>::kDB * 16 * kWave;
+template <int D>
+constexpr int kPartFloats = kPartOFloats<D> + 2 * kWave;
+
 template <int D, bool CAUSAL, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     const _Float16 *__restrict__ q, const _Float16 *__restrict__ k,
     const _Float16 *__restrict__ v, void *__restrict__ o, int seq,
-    int n_qtiles, int bh_count, int group, float c_scale, bool negate_q, bool split_all) {
+    int n_qtiles, int bh_count, int group, float c_scale, bool negate_q, bool split_all,
+    const PrefillPlan plan, float *__restrict__ part, unsigned *__restrict__ counters) {
   using G = Geo<D>;
   constexpr int kBc = G::kBc;
   constexpr int kKB = G::kKB;
@@ -610,8 +637,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   const int b_mirror = (grid & 7) == 0 ? grid - 8 * (b_id / 8 + 1) + (b_id & 7) : grid - 1 - b_id;
 #pragma unroll
   for (int round = 0; round < 2; ++round) {
-  const int pos = round == 0 ? b_id : grid + b_mirror;
-  if (pos >= n_items) break;
+  int pos, code = 0, split = 0;
+  if (plan.n_blocks > 0) {
+    const unsigned u = plan.unit[2 * b_id + round];
+    if (u == kNoUnit) break;
+    pos = static_cast<int>(u & 0xfffffu);
+    code = static_cast<int>((u >> 20) & 3u);
+    split = static_cast<int>(u >> 22);
+  } else {
+    pos = round == 0 ? b_id : grid + b_mirror;
+    if (pos >= n_items) break;
+  }
   // The previous item's last LDS accesses (output staging) end before this
   // item's loads overwrite the LDS.
   if (round > 0) __syncthreads();
@@ -629,9 +665,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
 
   const int key_end = CAUSAL ? min(seq, q0 + kBr) : seq;
   const int n_tiles = (key_end + kBc - 1) / kBc;
+  // This unit's tiles [tb, te): the whole range, or one chunk of it (tb is
+  // even, so each half keeps the parity of its tiles).
+  const int tb = code == 2 ? split_mid(n_tiles) : 0;
+  const int te = code == 1 ? split_mid(n_tiles) : n_tiles;
   ring.kp = k + kv_off;
   ring.vp = v + kv_off;
-  ring.n_tiles = n_tiles;
+  ring.t0 = tb;
+  ring.n_tiles = te;
   const int wave_key_end = CAUSAL ? min(seq, qw0 + kRowsPerWave) : seq;
   // Tiles [0, 2 n_main) need no mask for any row of the block, and all its
   // rows see >= kSplitPRowsBelow keys: each half runs n_main pipelined steps
@@ -643,9 +684,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // Pass 0 rounds P to fp16 once on rows that see enough keys; blocks whose
   // row sums then show a peaky row run again with split P on every tile.
   const bool short_rows = split_all || static_split;
-  const int main_tiles = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
-  const int n_main = main_tiles / 2;
-  const int n_steps = (n_tiles + 1) / 2;  // steps of the longer half
+  const int main_end = short_rows ? 0 : (CAUSAL ? q0 / kBc : seq / kBc);
+  const int n_main = max(0, min(main_end, te) - tb) / 2;
+  const int n_steps = (te - tb + 1) / 2;  // steps of the longer half
   // Rows that see many keys take the lazy max; shorter ones keep m at the
   // exact running max, whose P = 1 key takes no rounding.
   const float slack =
@@ -759,6 +800,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       else
         st.l = st.l * f0 + mlr[1] * f1;
       st.r = st.r * (f0 * f0) + mlr[2] * (f1 * f1);
+      st.m = m;  // O, l and r are now in units of the merged max
     }
     return xbase;
   };
@@ -901,6 +943,57 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }
   if (half == 1) continue;
 
+  if (code != 0) {
+    // ---- one chunk of a split item ---------------------------------------------
+    // Each row wave publishes its (O, m, l) partial, waits until it is stored
+    // and counts itself on the (item, row wave) counter; the second to arrive
+    // merges the other chunk's partial into its own (log-sum-exp rule) and
+    // writes the rows, then sets the counter back to zero.
+    float l_lane = kMfmaRowSum<D> ? st.lacc[0] : st.l;
+    float *mine = part + (static_cast<size_t>(2 * split + code - 1) * kRowWaves + rw) *
+                             kPartFloats<D>;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) store_coherent(mine + (db * 16 + a) * kWave + lane, st.o[db][a]);
+    store_coherent(mine + kPartOFloats<D> + lane, st.m);
+    store_coherent(mine + kPartOFloats<D> + kWave + lane, l_lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned *const counter = counters + kRowWaves * split + rw;
+    unsigned ticket = 0;
+    if (lane == 0)
+      ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __shfl(ticket, 0);
+    if (ticket == 0) continue;
+    const float *other = part + (static_cast<size_t>(2 * split + 2 - code) * kRowWaves + rw) *
+                                    kPartFloats<D>;
+    float o2[kDB][16];
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) o2[db][a] = load_coherent(other + (db * 16 + a) * kWave + lane);
+    const float m2 = load_coherent(other + kPartOFloats<D> + lane);
+    const float l2 = load_coherent(other + kPartOFloats<D> + kWave + lane);
+    // Both products rounded, then added (no fused multiply-add): the sum is
+    // the same whichever chunk arrives last, so the result does not depend on
+    // the order in which the two units finish.
+    const float m_all = fmaxf(st.m, m2);
+    const float f1 = fast_exp2(st.m - m_all), f2 = fast_exp2(m2 - m_all);
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) st.o[db][a] = st.o[db][a] * f1 + o2[db][a] * f2;
+      l_lane = l_lane * f1 + l2 * f2;
+    }
+    if constexpr (kMfmaRowSum<D>)
+      st.lacc[0] = l_lane;
+    else
+      st.l = l_lane;
+    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   // ---- epilogue: O = O^T / l --------------------------------------------------
   // Each lane holds one query row; it writes its row's values to this row
   // wave's staging area, then the wave stores whole rows: lane i of a store
@@ -953,25 +1046,192 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   }  // items
 }
 
+// ---- host: the unit plan --------------------------------------------------------
+// Cost of a unit in pipeline steps: its tiles over the two halves, plus what
+// every unit pays once (Q and the first tiles in flight, the half merge, the
+// epilogue), plus the partial store and merge of a chunk.
+constexpr int kUnitOverheadSteps = 3;
+constexpr int kChunkOverheadSteps = 1;
+constexpr int kMinSplitTiles = 8;  // items with fewer tiles stay whole
+
+struct PlanShape {
+  int bh, n_qtiles, seq, causal, kbc, group, cu;
+  bool operator<(const PlanShape &o) const {
+    return std::tie(bh, n_qtiles, seq, causal, kbc, group, cu) <
+           std::tie(o.bh, o.n_qtiles, o.seq, o.causal, o.kbc, o.group, o.cu);
+  }
+};
+struct PlanEntry {
+  PrefillPlan plan;
+  int n_splits;
+};
+
+int item_tiles(const PlanShape &s, int pos) {
+  const int qtile = s.n_qtiles - 1 - pos / s.bh;
+  const int key_end = s.causal ? std::min(s.seq, qtile * kBr + kBr) : s.seq;
+  return (key_end + s.kbc - 1) / s.kbc;
+}
+
+struct PlanUnit {
+  int cost;
+  unsigned code;
+};
+
+// Units of the plan that splits the n_split heaviest items, heaviest unit
+// first. Items are numbered heaviest query tile first; the split ones are
+// the first n_split in (query tile, head) order, so whether an item is split
+// depends on its head and query tile only, not on the block placement (a
+// grouped-query call splits the same items as one on repeated K/V heads).
+void plan_units(const PlanShape &s, int n_split, std::vector<PlanUnit> &units) {
+  units.clear();
+  const int n_items = s.bh * s.n_qtiles;
+  for (int pos = 0; pos < n_items; ++pos) {
+    const int nt = item_tiles(s, pos);
+    int head = home_head(pos, s.bh);
+    if (s.group > 1) head = grouped_head(head, s.bh);
+    const int rank = (pos / s.bh) * s.bh + head;  // (query tile, head) order
+    if (rank < n_split) {
+      const int mid = split_mid(nt);
+      const unsigned base = static_cast<unsigned>(pos) | (static_cast<unsigned>(rank) << 22);
+      units.push_back({(mid + 1) / 2 + kUnitOverheadSteps + kChunkOverheadSteps, base | (1u << 20)});
+      units.push_back(
+          {(nt - mid + 1) / 2 + kUnitOverheadSteps + kChunkOverheadSteps, base | (2u << 20)});
+    } else {
+      units.push_back({(nt + 1) / 2 + kUnitOverheadSteps, static_cast<unsigned>(pos)});
+    }
+  }
+  std::stable_sort(units.begin(), units.end(),
+                   [](const PlanUnit &a, const PlanUnit &b) { return a.cost > b.cost; });
+}
+
+// Longest unit time of any block when the `g` blocks take the units heaviest
+// first: the 2 g - n heaviest alone, the others paired heaviest with lightest.
+int plan_makespan(const std::vector<PlanUnit> &units, int g) {
+  const int n = static_cast<int>(units.size());
+  const int singles = std::max(0, 2 * g - n);
+  int span = 0;
+  for (int i = 0; i < std::min(singles, n); ++i) span = std::max(span, units[i].cost);
+  for (int i = singles, j = n - 1; i < j; ++i, --j) span = std::max(span, units[i].cost + units[j].cost);
+  return span;
+}
+
+// The plan for one shape (cached): the number of split items that minimises
+// the makespan, or no plan when splitting does not shorten it.
+const PlanEntry &prefill_plan(const PlanShape &s) {
+  static std::mutex mu;
+  static std::map<PlanShape, PlanEntry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(s);
+  if (it != cache.end()) return it->second;
+  PlanEntry e{};
+  e.plan.n_blocks = 0;
+  e.n_splits = 0;
+  const long long n_items = static_cast<long long>(s.bh) * s.n_qtiles;
+  const int g = s.cu;
+  if (g > 0 && g <= kPlanMaxBlocks && n_items <= 2LL * g) {
+    std::vector<PlanUnit> units;
+    plan_units(s, 0, units);
+    int best_span = plan_makespan(units, g), best_k = 0;
+    const int k_max = static_cast<int>(std::min<long long>(n_items, 2LL * g - n_items));
+    for (int kk = 1; kk <= k_max && item_tiles(s, kk - 1) >= kMinSplitTiles; ++kk) {
+      plan_units(s, kk, units);
+      const int span = plan_makespan(units, g);
+      if (span < best_span) {
+        best_span = span;
+        best_k = kk;
+      }
+    }
+    if (best_k > 0 && static_cast<size_t>(kRowWaves) * best_k <= kMergeCountersPerSlot) {
+      plan_units(s, best_k, units);
+      const int n = static_cast<int>(units.size());
+      const int singles = std::max(0, 2 * g - n);
+      e.plan.n_blocks = g;
+      e.n_splits = best_k;
+      for (int b = 0; b < g; ++b) e.plan.unit[2 * b] = e.plan.unit[2 * b + 1] = kNoUnit;
+      // Blocks go to the 8 XCDs round-robin (block b on XCD b % 8), and the
+      // head of item pos is placed (home_head) for XCD pos % 8. A block is
+      // taken on its heavier unit's XCD while one is free there; its lighter
+      // unit is, among the remaining units of the cost the pairing asks for,
+      // one of that XCD when there is one. So most units of a head share an
+      // L2, as on the formula path.
+      const auto xcd_of = [](unsigned code) { return static_cast<int>(code & 0xfffffu) % 8; };
+      std::vector<int> free_b[8];
+      for (int b = g - 1; b >= 0; --b) free_b[b % 8].push_back(b);
+      const auto take_block = [&](int x) {
+        for (int d = 0; d < 8; ++d) {
+          std::vector<int> &f = free_b[(x + d) % 8];
+          if (!f.empty()) {
+            const int b = f.back();
+            f.pop_back();
+            return b;
+          }
+        }
+        return -1;  // unreachable: at most g blocks are taken
+      };
+      for (int i = 0; i < singles && i < n; ++i) e.plan.unit[2 * take_block(xcd_of(units[i].code))] = units[i].code;
+      const int n_pairs = (n - std::min(singles, n)) / 2;
+      std::map<int, std::vector<unsigned>> light[8];  // cost -> codes, per XCD
+      for (int j = n - n_pairs; j < n; ++j) light[xcd_of(units[j].code)][units[j].cost].push_back(units[j].code);
+      for (int k = 0; k < n_pairs; ++k) {
+        const unsigned heavy = units[singles + k].code;
+        const int x = xcd_of(heavy);
+        const int cost = units[n - 1 - k].cost;  // the k-th lightest unit's cost
+        unsigned lite = kNoUnit;
+        for (int d = 0; d < 8 && lite == kNoUnit; ++d) {
+          auto it = light[(x + d) % 8].find(cost);
+          if (it != light[(x + d) % 8].end() && !it->second.empty()) {
+            lite = it->second.back();
+            it->second.pop_back();
+          }
+        }
+        const int b = take_block(x);
+        e.plan.unit[2 * b] = heavy;
+        e.plan.unit[2 * b + 1] = lite;
+      }
+    }
+  }
+  return cache.emplace(s, e).first->second;
+}
+
+template <int D>
+size_t plan_workspace_bytes(const PlanEntry &e) {
+  return static_cast<size_t>(e.n_splits) * 2 * kRowWaves * kPartFloats<D> * sizeof(float);
+}
+
+int current_cu_count() {
+  int dev = 0;
+  return hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
+}
+
 template <int D, bool CAUSAL, bool OUT_F32>
 void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
                 int seq, int group, float c_scale, bool negate_q, bool split_all,
-                hipStream_t stream) {
+                void *workspace, size_t workspace_bytes, hipStream_t stream) {
   const int n_qtiles = (seq + kBr - 1) / kBr;
   const long long items = static_cast<long long>(bh) * n_qtiles;
-  // A block takes a whole CU's LDS and up to two items: one block per CU,
-  // or half the items when there are more than two per CU; without a CU
-  // count, one block per item.
-  int dev = 0;
-  const int cu = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
+  const int cu = current_cu_count();
+  // With a plan (and its workspace and counters): one block per CU. Otherwise
+  // a block takes a whole CU's LDS and up to two items: one block per CU, or
+  // half the items when there are more than two per CU; without a CU count,
+  // one block per item.
+  const PlanEntry &e = prefill_plan({bh, n_qtiles, seq, CAUSAL ? 1 : 0, Geo<D>::kBc, group, cu});
+  unsigned *counters = nullptr;
+  const PrefillPlan *plan = nullptr;
+  static const PrefillPlan no_plan{0, {}};
+  if (e.plan.n_blocks > 0 && workspace != nullptr && workspace_bytes >= plan_workspace_bytes<D>(e))
+    counters = merge_counters(stream, static_cast<size_t>(kRowWaves) * e.n_splits);
+  if (counters != nullptr) plan = &e.plan;
   const unsigned blocks = static_cast<unsigned>(
-      cu > 0 ? std::min<long long>(items, std::max<long long>(cu, (items + 1) / 2)) : items);
+      plan != nullptr ? plan->n_blocks
+      : cu > 0        ? std::min<long long>(items, std::max<long long>(cu, (items + 1) / 2))
+                      : items);
   hipLaunchKernelGGL((prefill_kernel<D, CAUSAL, OUT_F32>), dim3(blocks),
                      dim3(kThreads), 0, stream,
                      static_cast<const _Float16 *>(q),
                      static_cast<const _Float16 *>(k),
                      static_cast<const _Float16 *>(v), o, seq, n_qtiles, bh, group,
-                     c_scale, negate_q, split_all);
+                     c_scale, negate_q, split_all, plan != nullptr ? *plan : no_plan,
+                     static_cast<float *>(workspace), counters);
 }
 
 }  // namespace
@@ -979,27 +1239,41 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
 template <int D>
 void launch_d(const void *q, const void *k, const void *v, void *o, bool out_f32, int bh,
               int seq, int group, bool causal, float c_scale, bool negate_q, bool split_all,
-              hipStream_t stream) {
+              void *ws, size_t ws_bytes, hipStream_t stream) {
   if (causal) {
     if (out_f32)
-      launch_one<D, true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
-                                stream);
+      launch_one<D, true, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all, ws,
+                                ws_bytes, stream);
     else
-      launch_one<D, true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
-                                 stream);
+      launch_one<D, true, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all, ws,
+                                 ws_bytes, stream);
   } else {
     if (out_f32)
-      launch_one<D, false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
-                                 stream);
+      launch_one<D, false, true>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all, ws,
+                                 ws_bytes, stream);
     else
-      launch_one<D, false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all,
-                                  stream);
+      launch_one<D, false, false>(q, k, v, o, bh, seq, group, c_scale, negate_q, split_all, ws,
+                                  ws_bytes, stream);
   }
+}
+
+size_t prefill_workspace_bytes(int batch, int heads, int seq, bool causal) {
+  if (batch <= 0 || heads <= 0 || seq <= 0) return 0;
+  const int bh = batch * heads;
+  const int n_qtiles = (seq + kBr - 1) / kBr;
+  const int cu = current_cu_count();
+  const int c = causal ? 1 : 0;
+  // The number of split items depends on the shape only (not on the K/V
+  // grouping, which only permutes the heads among the blocks).
+  return std::max(
+      plan_workspace_bytes<64>(prefill_plan({bh, n_qtiles, seq, c, Geo<64>::kBc, 1, cu})),
+      plan_workspace_bytes<128>(prefill_plan({bh, n_qtiles, seq, c, Geo<128>::kBc, 1, cu})));
 }
 
 int launch_prefill(const void *q, const void *k, const void *v, void *o,
                    bool out_f32, int batch, int heads, int kv_heads, int seq,
-                   int head_dim, bool causal, float scale, hipStream_t stream) {
+                   int head_dim, bool causal, float scale, void *workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
   const int bh = batch * heads;
   const int group = heads / kv_heads;
   const float c_scale = fabsf(scale) * kLog2e;
@@ -1012,10 +1286,10 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
   const bool split_all = fabsf(scale) * sqrtf(static_cast<float>(head_dim)) > kSplitAllWidth;
   if (head_dim == 128)
     launch_d<128>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, split_all,
-                  stream);
+                  workspace, workspace_bytes, stream);
   else
     launch_d<64>(q, k, v, o, out_f32, bh, seq, group, causal, c_scale, negate_q, split_all,
-                 stream);
+                 workspace, workspace_bytes, stream);
   return check_hip(hipGetLastError(), "prefill_kernel launch");
 }
 

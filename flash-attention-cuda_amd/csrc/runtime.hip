@@ -166,7 +166,9 @@ int fa_decode_min_blocks(int device, int *min_blocks) {
   return FA_OK;
 }
 
-size_t fa_prefill_workspace_bytes(int, int, int, int) { return 0; }
+size_t fa_prefill_workspace_bytes(int batch, int heads, int seq, int causal) {
+  return prefill_workspace_bytes(batch, heads, seq, causal != 0);
+}
 
 namespace {
 int check_groups(int heads, int kv_heads) {
@@ -178,7 +180,7 @@ int check_groups(int heads, int kv_heads) {
 
 int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_dtype,
                  int batch, int heads, int kv_heads, int seq, int head_dim, int causal,
-                 float scale, void *stream) {
+                 float scale, void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
   if (head_dim != 64 && head_dim != 128)
     return set_error(FA_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128, got %d", head_dim);
@@ -202,7 +204,8 @@ int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_d
   if (!std::isfinite(scale) || !std::isfinite(scale * 1.4426950408889634f))
     return set_error(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
   return launch_prefill(q, k, v, o, out_dtype == FA_OUT_F32, batch, heads, kv_heads, seq,
-                        head_dim, causal != 0, scale, static_cast<hipStream_t>(stream));
+                        head_dim, causal != 0, scale, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
 }
 
 // Resolves split_size 0 to the automatic choice; returns an fa_status.
@@ -323,28 +326,22 @@ int fa_prefill(const void *q, const void *k, const void *v, void *o,
                int out_dtype, int batch, int heads, int seq, int causal,
                float scale, void *workspace, size_t workspace_bytes,
                void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   return prefill_impl(q, k, v, o, out_dtype, batch, heads, heads, seq, 64, causal, scale,
-                      stream);
+                      workspace, workspace_bytes, stream);
 }
 
 int fa_prefill_gqa(const void *q, const void *k, const void *v, void *o, int out_dtype,
                    int batch, int heads, int kv_heads, int seq, int causal, float scale,
                    void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, 64, causal, scale,
-                      stream);
+                      workspace, workspace_bytes, stream);
 }
 
 int fa_prefill_hd(const void *q, const void *k, const void *v, void *o, int out_dtype,
                   int batch, int heads, int kv_heads, int seq, int head_dim, int causal,
                   float scale, void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   return prefill_impl(q, k, v, o, out_dtype, batch, heads, kv_heads, seq, head_dim, causal,
-                      scale, stream);
+                      scale, workspace, workspace_bytes, stream);
 }
 
 size_t fa_decode_workspace_bytes(int batch, int heads, int max_seq,

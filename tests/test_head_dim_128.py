@@ -194,6 +194,7 @@ def _capi():
                                    "libflashattn_hip.so"))
     lib.fa_last_error.restype = ctypes.c_char_p
     lib.fa_decode_hd_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_prefill_workspace_bytes.restype = ctypes.c_size_t
     return lib
 
 
@@ -208,8 +209,12 @@ def test_capi_prefill_hd_and_decode_hd_match_python_api():
     k = torch.randn(2, 3, 300, D, generator=g).half().cuda()
     v = torch.randn(2, 3, 300, D, generator=g).half().cuda()
     o = torch.empty_like(q)
+    # With the workspace the Python API allocates, the C ABI takes the same
+    # work split and gives the same bits.
+    ws_bytes = lib.fa_prefill_workspace_bytes(2, 6, 300, 1)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
     rc = lib.fa_prefill_hd(ptr(q), ptr(k), ptr(v), ptr(o), 0, 2, 6, 3, 300, D, 1,
-                           ctypes.c_float(SCALE), None, ctypes.c_size_t(0), stream)
+                           ctypes.c_float(SCALE), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     assert rc == 0, lib.fa_last_error()
     torch.cuda.synchronize()
     assert torch.equal(o, flashattn_cuda.prefill_gqa(q, k, v, True, SCALE))

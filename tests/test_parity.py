@@ -580,6 +580,7 @@ def capi():
     dll = ctypes.CDLL(LIB)
     dll.fa_last_error.restype = ctypes.c_char_p
     dll.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+    dll.fa_prefill_workspace_bytes.restype = ctypes.c_size_t
     return dll
 
 
@@ -593,6 +594,38 @@ def test_capi_prefill_matches_python_api(capi):
     assert rc == 0, capi.fa_last_error()
     torch.cuda.synchronize()
     assert torch.equal(o, flashattn_cuda.prefill(q, k, v, True, SCALE))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_capi_prefill_with_and_without_workspace(capi, causal):
+    """A shape whose heaviest query tiles are split over two CUs when the
+    call brings fa_prefill_workspace_bytes of workspace (the Python API
+    does): with it the C ABI gives the Python API's bits; without it every
+    item runs whole on one CU. Both within the bound of the oracle, fp16
+    and fp32 outputs."""
+    B, H, S = 1, 2, 1280
+    q, k, v = oracle.make_prefill_inputs(B, H, S, seed=16)
+    ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    ws_bytes = capi.fa_prefill_workspace_bytes(B, H, S, int(causal))
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    outs = {}
+    for use_ws in (True, False):
+        for dtype, code in ((torch.float16, 0), (torch.float32, 1)):
+            o = torch.empty(q.shape, dtype=dtype, device="cuda")
+            rc = capi.fa_prefill(p(qd), p(kd), p(vd), p(o), code, B, H, S, int(causal),
+                                 ctypes.c_float(SCALE), p(ws) if use_ws else None,
+                                 ctypes.c_size_t(ws_bytes if use_ws else 0), stream)
+            assert rc == 0, capi.fa_last_error()
+            outs[use_ws, code] = o
+    torch.cuda.synchronize()
+    assert torch.equal(outs[True, 0], flashattn_cuda.prefill(qd, kd, vd, causal, SCALE))
+    for use_ws in (True, False):
+        _check(outs[use_ws, 0], outs[use_ws, 1], ref,
+               f"S={S} causal={causal} {'split' if use_ws else 'whole'} items")
 
 
 def test_capi_decode_matches_python_api(capi):
