@@ -916,16 +916,17 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   const int bh = b * heads + h;
   const int sub = lane / RowGeo<D>::kLanesPerRow;    // row inside a row group
   const int slice = lane % RowGeo<D>::kLanesPerRow;  // head dims [8 * slice, +8)
-  // The query is loaded here, with the lengths, so both loads are in flight
-  // together.
+  // The query load is issued first; after a ranking the lengths come from
+  // LDS, so the first cache loads wait for no other memory round trip.
   half2 qh[4];
   load_query<D>(q, bh, slice, qh);
-  const int len = max(0, min(seq_lens[b], max_seq));
+  const int len = ranked ? s_len[b] : max(0, min(seq_lens[b], max_seq));
   if (chunk == 0) {
     int rows_per_wave;
     if (target_waves > 0) {
       int part = 0;
-      for (int t = lane; t < batch; t += kWave) part += max(0, min(seq_lens[t], max_seq));
+      for (int t = lane; t < batch; t += kWave)
+        part += ranked ? s_len[t] : max(0, min(seq_lens[t], max_seq));
 #pragma unroll
       for (int off = kWave / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
       const float total = static_cast<float>(__builtin_amdgcn_readfirstlane(part));
