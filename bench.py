@@ -167,7 +167,8 @@ def bench_prefill(fa, batch, heads, seq, causal, protocol="ref", steps=0, warmup
     q, k, v = (t.cuda() for t in cpu_inputs_prefill(batch, heads, seq, d=d))
     n = copies_for(3 * q.numel() * 2) if protocol == "ref" else 1
     sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
-    fns = [lambda s=s: fa.prefill(s[0], s[1], s[2], causal, SCALE) for s in sets]
+    scale = d ** -0.5  # 1/sqrt(head_dim): the reference's 0.125 at head_dim 64
+    fns = [lambda s=s: fa.prefill(s[0], s[1], s[2], causal, scale) for s in sets]
     torch.cuda.synchronize()
     flops = attention_flops(batch, heads, seq, causal, d)
     if protocol == "ref":
@@ -186,7 +187,8 @@ def bench_decode(fa, batch, heads, lmax, lens=None, protocol="ref", steps=0, war
     q, k, v, rl = q.cuda(), k.cuda(), v.cuda(), rl.cuda()
     n = copies_for(2 * k.numel() * 2)
     sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
-    fns = [lambda s=s: fa.decode(s[0], s[1], s[2], rl, SCALE) for s in sets]
+    scale = d ** -0.5
+    fns = [lambda s=s: fa.decode(s[0], s[1], s[2], rl, scale) for s in sets]
     torch.cuda.synchronize()
     nbytes = decode_bytes(heads, rl.cpu(), lmax, d)
     if protocol == "ref":
@@ -243,7 +245,8 @@ def bench_gqa(fa):
 
 def bench_head_dim_128(fa):
     """head_dim 128 (the reference's named next step, README.md:397) at the
-    config 3, config 2 (full) and config 5 shapes, reference timing protocol.
+    config 3, config 2 (full) and config 5 shapes, reference timing protocol,
+    at the standard scale 1/sqrt(128) (the configs' 0.125 is 1/sqrt(64)).
     FLOPs 4 B H S^2 128 (halved when causal); decode bytes count the K/V rows
     read (256 B each per head), q, o and seq_lens."""
     rows = []
@@ -273,9 +276,10 @@ def bench_head_dim_128(fa):
     sets += [tuple(t.clone() for t in sets[0]) for _ in range(n - 1)]
     torch.cuda.synchronize()
     nbytes = decode_bytes(kv_heads, rl.cpu(), 4096, 128) + 2 * 32 * (heads - kv_heads) * 128 * 2
-    ms = ref_timeit([lambda s=s: fa.decode_gqa(qd, s[0], s[1], rl, SCALE) for s in sets])
+    scale = 128 ** -0.5
+    ms = ref_timeit([lambda s=s: fa.decode_gqa(qd, s[0], s[1], rl, scale) for s in sets])
     ms_rep = ref_timeit([lambda s=s: fa.decode(qd, s[0].repeat_interleave(group, 1),
-                                               s[1].repeat_interleave(group, 1), rl, SCALE)
+                                               s[1].repeat_interleave(group, 1), rl, scale)
                          for s in sets])
     rows.append({"config": "C5-shape GQA ragged decode B32 H14 Hkv2 Lmax4096 D128", "ms": ms,
                  "gbs": nbytes / (ms * 1e-3) / 1e9,

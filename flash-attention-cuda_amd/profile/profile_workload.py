@@ -38,14 +38,14 @@ WORKLOADS = {
                           "flop", 4.0 * 4 * 12 * 1024 * 1024 * 64 / 2),
     "prefill_c2_full": ("config 2: full prefill B=4 H=12 S=1024", "prefill_kernel<64, false",
                         "flop", 4.0 * 4 * 12 * 1024 * 1024 * 64),
-    "prefill_c3_d128": ("config 3 shape at head_dim 128: causal prefill B=1 H=14 S=4096 D=128",
+    "prefill_c3_d128": ("config 3 shape at head_dim 128: causal prefill B=1 H=14 S=4096 D=128, scale 1/sqrt(128)",
                         "prefill_kernel<128, true", "flop", 4.0 * 14 * 4096 * 4096 * 128 / 2),
     "decode_c4": ("config 4: decode B=1 H=12 L=4096 (split-K, merged in the same launch)",
                   "decode_split_fused_kernel",
                   "byte", 2 * 12 * 64 * 2 * 4096 + 2 * 12 * 64 * 2 + 4),
     "decode_c5": ("config 5: ragged decode B=32 H=14 Lmax=4096, lens U[1,4096] seed 0",
                   "decode_bh_kernel", "byte", 2 * 14 * 64 * 2 * 73374 + 2 * 32 * 14 * 64 * 2 + 128),
-    "decode_c5_d128": ("config 5 shape at head_dim 128: ragged decode B=32 H=14 Lmax=4096 D=128",
+    "decode_c5_d128": ("config 5 shape at head_dim 128: ragged decode B=32 H=14 Lmax=4096 D=128, scale 1/sqrt(128)",
                        "decode_bh_kernel<128", "byte",
                        2 * 14 * 128 * 2 * 73374 + 2 * 32 * 14 * 128 * 2 + 128),
     "decode_gqa_c5": ("config 5 batch with 2 K/V heads (group 7): grouped decode",
@@ -86,7 +86,7 @@ def _prefill(batch, heads, seq, causal, d=64):
     g = torch.Generator().manual_seed(0)
     shape = (batch, heads, seq, d)
     q, k, v = (torch.randn(shape, generator=g).half().cuda() for _ in range(3))
-    _run([lambda: fa.prefill(q, k, v, causal, SCALE)])
+    _run([lambda: fa.prefill(q, k, v, causal, d ** -0.5)])  # 0.125 = SCALE at d = 64
 
 
 def _decode_inputs(batch, heads, lmax, lens=None, d=64):
@@ -117,7 +117,7 @@ def _decode(batch, heads, lmax, lens=None, kv_every=1, d=64):
     q, rl = q.cuda(), rl.cuda()
     n = _copies(2 * k.numel() * 2)  # rotate caches through more than 2x the MALL
     sets = [(k.cuda(), v.cuda()) for _ in range(n)]
-    _run([lambda s=s: call(q, s[0], s[1], rl, SCALE) for s in sets])
+    _run([lambda s=s: call(q, s[0], s[1], rl, d ** -0.5) for s in sets])
 
 
 def _copy():
