@@ -49,6 +49,9 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
 // Workspace that lets launch_prefill split items for this shape on the
 // current device (either head size), 0 when it would not split.
 size_t prefill_workspace_bytes(int batch, int heads, int seq, bool causal);
+// The host's unit plan for a prefill shape on a `cu`-CU device (fa_prefill_plan_units).
+int prefill_plan_units(int bh, int seq, int causal, int head_dim, int group, int cu,
+                       unsigned *units, int cap, int *n_blocks, int *n_splits);
 // head_dim is 64 or 128; grouped queries take the matrix-core grouped pass
 // and the merge, the others the VALU split-K / whole-sequence kernels.
 int launch_decode(const void *q, const void *k_cache, const void *v_cache,

@@ -1104,44 +1104,83 @@ void plan_units(const PlanShape &s, int n_split, std::vector<PlanUnit> &units) {
                    [](const PlanUnit &a, const PlanUnit &b) { return a.cost > b.cost; });
 }
 
-// Longest unit time of any block when the `g` blocks take the units heaviest
-// first: the 2 g - n heaviest alone, the others paired heaviest with lightest.
-int plan_makespan(const std::vector<PlanUnit> &units, int g) {
-  const int n = static_cast<int>(units.size());
-  const int singles = std::max(0, 2 * g - n);
-  int span = 0;
-  for (int i = 0; i < std::min(singles, n); ++i) span = std::max(span, units[i].cost);
-  for (int i = singles, j = n - 1; i < j; ++i, --j) span = std::max(span, units[i].cost + units[j].cost);
+// Unit costs of the plan that splits the first n_split items in (query tile,
+// head) order, as a histogram (cnt[c] units of cost c); returns the unit count.
+// All heads of a query tile have the same tiles, so this is per tile level.
+int plan_costs(const PlanShape &s, int n_split, std::vector<int> &cnt) {
+  std::fill(cnt.begin(), cnt.end(), 0);
+  int n = 0;
+  for (int level = 0; level < s.n_qtiles; ++level) {
+    const int nt = item_tiles(s, level * s.bh);
+    const int split = std::min(s.bh, std::max(0, n_split - level * s.bh));
+    const int mid = split_mid(nt);
+    const int whole = (nt + 1) / 2 + kUnitOverheadSteps;
+    const int first = (mid + 1) / 2 + kUnitOverheadSteps + kChunkOverheadSteps;
+    const int second = (nt - mid + 1) / 2 + kUnitOverheadSteps + kChunkOverheadSteps;
+    cnt[whole] += s.bh - split;
+    cnt[first] += split;
+    cnt[second] += split;
+    n += s.bh + split;
+  }
+  return n;
+}
+
+// Longest unit time of any block when the `g` blocks take the n units
+// heaviest first: the 2 g - n heaviest alone, the others paired heaviest with
+// lightest (from the cost histogram, which it consumes).
+int plan_makespan(std::vector<int> &cnt, int n, int g) {
+  int singles = std::max(0, 2 * g - n);
+  int hi = static_cast<int>(cnt.size()) - 1, lo = 0, span = 0;
+  while (hi >= 0 && singles > 0) {  // the heaviest units, alone
+    if (cnt[hi] == 0) {
+      --hi;
+      continue;
+    }
+    span = std::max(span, hi);
+    const int take = std::min(cnt[hi], singles);
+    cnt[hi] -= take;
+    singles -= take;
+  }
+  for (;;) {  // the rest, heaviest with lightest
+    while (hi >= 0 && cnt[hi] == 0) --hi;
+    while (lo < static_cast<int>(cnt.size()) && cnt[lo] == 0) ++lo;
+    if (hi < 0 || lo > hi) break;
+    if (lo == hi) {
+      span = std::max(span, cnt[hi] >= 2 ? 2 * hi : hi);
+      break;
+    }
+    span = std::max(span, hi + lo);
+    const int take = std::min(cnt[hi], cnt[lo]);
+    cnt[hi] -= take;
+    cnt[lo] -= take;
+  }
   return span;
 }
 
-// The plan for one shape (cached): the number of split items that minimises
-// the makespan, or no plan when splitting does not shorten it.
-const PlanEntry &prefill_plan(const PlanShape &s) {
-  static std::mutex mu;
-  static std::map<PlanShape, PlanEntry> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(s);
-  if (it != cache.end()) return it->second;
+// The plan for one shape: the number of split items that minimises the
+// makespan (from the cost histograms, O(levels + max cost) per candidate), or
+// no plan when splitting does not shorten it.
+PlanEntry make_plan(const PlanShape &s) {
   PlanEntry e{};
   e.plan.n_blocks = 0;
   e.n_splits = 0;
   const long long n_items = static_cast<long long>(s.bh) * s.n_qtiles;
   const int g = s.cu;
   if (g > 0 && g <= kPlanMaxBlocks && n_items <= 2LL * g) {
-    std::vector<PlanUnit> units;
-    plan_units(s, 0, units);
-    int best_span = plan_makespan(units, g), best_k = 0;
+    std::vector<int> cnt((item_tiles(s, 0) + 1) / 2 + kUnitOverheadSteps + kChunkOverheadSteps + 1);
+    int n = plan_costs(s, 0, cnt);
+    int best_span = plan_makespan(cnt, n, g), best_k = 0;
     const int k_max = static_cast<int>(std::min<long long>(n_items, 2LL * g - n_items));
     for (int kk = 1; kk <= k_max && item_tiles(s, kk - 1) >= kMinSplitTiles; ++kk) {
-      plan_units(s, kk, units);
-      const int span = plan_makespan(units, g);
+      n = plan_costs(s, kk, cnt);
+      const int span = plan_makespan(cnt, n, g);
       if (span < best_span) {
         best_span = span;
         best_k = kk;
       }
     }
     if (best_k > 0 && static_cast<size_t>(kRowWaves) * best_k <= kMergeCountersPerSlot) {
+      std::vector<PlanUnit> units;
       plan_units(s, best_k, units);
       const int n = static_cast<int>(units.size());
       const int singles = std::max(0, 2 * g - n);
@@ -1190,7 +1229,22 @@ const PlanEntry &prefill_plan(const PlanShape &s) {
       }
     }
   }
-  return cache.emplace(s, e).first->second;
+  return e;
+}
+
+// Plans are kept per shape (a few KiB each); the cache starts over when it
+// holds kPlanCacheShapes of them, so a caller cycling through many shapes
+// neither grows it without bound nor pays more than one plan per shape and
+// round.
+constexpr size_t kPlanCacheShapes = 256;
+PlanEntry prefill_plan(const PlanShape &s) {
+  static std::mutex mu;
+  static std::map<PlanShape, PlanEntry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(s);
+  if (it != cache.end()) return it->second;
+  if (cache.size() >= kPlanCacheShapes) cache.clear();
+  return cache.emplace(s, make_plan(s)).first->second;
 }
 
 template <int D>
@@ -1214,7 +1268,7 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
   // a block takes a whole CU's LDS and up to two items: one block per CU, or
   // half the items when there are more than two per CU; without a CU count,
   // one block per item.
-  const PlanEntry &e = prefill_plan({bh, n_qtiles, seq, CAUSAL ? 1 : 0, Geo<D>::kBc, group, cu});
+  const PlanEntry e = prefill_plan({bh, n_qtiles, seq, CAUSAL ? 1 : 0, Geo<D>::kBc, group, cu});
   unsigned *counters = nullptr;
   const PrefillPlan *plan = nullptr;
   static const PrefillPlan no_plan{0, {}};
@@ -1312,6 +1366,20 @@ int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n) {
     }
     ++*n;
   }
+  return FA_OK;
+}
+
+int prefill_plan_units(int bh, int seq, int causal, int head_dim, int group, int cu,
+                       unsigned *units, int cap, int *n_blocks, int *n_splits) {
+  if (bh <= 0 || seq <= 0 || group <= 0 || (head_dim != 64 && head_dim != 128) || cu < 0 ||
+      cap < 0 || (cap > 0 && units == nullptr) || n_blocks == nullptr || n_splits == nullptr)
+    return set_error(FA_ERR_INVALID_ARGUMENT, "invalid prefill plan query");
+  const int n_qtiles = (seq + kBr - 1) / kBr;
+  const PlanEntry e = prefill_plan(
+      {bh, n_qtiles, seq, causal ? 1 : 0, head_dim == 64 ? Geo<64>::kBc : Geo<128>::kBc, group, cu});
+  *n_blocks = e.plan.n_blocks;
+  *n_splits = e.n_splits;
+  for (int i = 0; i < std::min(cap, 2 * e.plan.n_blocks); ++i) units[i] = e.plan.unit[i];
   return FA_OK;
 }
 

@@ -170,6 +170,13 @@ size_t fa_prefill_workspace_bytes(int batch, int heads, int seq, int causal) {
   return prefill_workspace_bytes(batch, heads, seq, causal != 0);
 }
 
+int fa_prefill_plan_units(int batch_heads, int seq, int causal, int head_dim, int group, int cu,
+                          unsigned *units, int cap, int *n_blocks, int *n_splits) {
+  clear_error();
+  return prefill_plan_units(batch_heads, seq, causal, head_dim, group, cu, units, cap, n_blocks,
+                            n_splits);
+}
+
 namespace {
 int check_groups(int heads, int kv_heads) {
   if (kv_heads <= 0 || kv_heads > heads || heads % kv_heads != 0)

@@ -40,6 +40,8 @@
  *                               fa_decode_gqa / fa_kv_append.
  *   fa_decode_hd_noalloc     <- no counterpart: fa_decode_hd without a workspace
  *                               argument, for callers that cannot allocate.
+ *   fa_prefill_plan_units    <- no counterpart: reads this build's prefill work-unit
+ *                               plan (tests, tools); launches nothing.
  *   fa_legacy_attention      <- launch_naive_attention / launch_tiled_attention /
  *                               launch_fused_attention,
  *                               src/legacy/{naive,tiled,fused}_attention.cu
@@ -112,8 +114,23 @@ int fa_choose_decode_split(int max_seq, int batch, int heads, int min_blocks);
  * 2 * (compute units), as the reference. Returns an fa_status. */
 int fa_decode_min_blocks(int device, int *min_blocks);
 
-/* Bytes of device workspace fa_prefill needs for this shape (may be 0). */
+/* Bytes of device workspace that let fa_prefill (and the _gqa / _hd entry
+ * points, sized for head_dim 128) split the heaviest query tiles' key ranges
+ * over two CUs for this shape on the current device; 0 when the shape gains
+ * nothing. Every prefill entry point also runs with no workspace. */
 size_t fa_prefill_workspace_bytes(int batch, int heads, int seq, int causal);
+
+/* No counterpart in the reference (it inspects this build's host planner,
+ * for tests and tools): the work units a prefill of batch_heads = B * H
+ * query heads, K/V grouping `group` (H / H_kv), would run on a device of `cu`
+ * compute units when given its workspace. *n_blocks = 0 means no plan (every
+ * item runs whole). Otherwise block b runs units[2 b] and then units[2 b + 1]
+ * (0xffffffff: none), each pos | code << 20 | split << 22: item pos (query
+ * tile n_qtiles - 1 - pos / batch_heads), code 0 for all its keys, 1 / 2 for
+ * the first / second key chunk, split < *n_splits its partial slot. Writes at
+ * most `cap` entries. Needs no GPU. */
+int fa_prefill_plan_units(int batch_heads, int seq, int causal, int head_dim, int group, int cu,
+                          unsigned *units, int cap, int *n_blocks, int *n_splits);
 
 /* o = softmax(q k^T * scale [+ causal mask]) v for every (b, h).
  * causal: query row i attends keys 0..i. fp32 accumulation throughout.

@@ -66,6 +66,7 @@ def test_header_declares_the_expected_entry_points():
             "fa_prefill",
             "fa_prefill_gqa",
             "fa_prefill_hd",
+            "fa_prefill_plan_units",
             "fa_prefill_workspace_bytes",
             "fa_version",
         ]
