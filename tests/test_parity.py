@@ -628,6 +628,47 @@ def test_capi_prefill_with_and_without_workspace(capi, causal):
                f"S={S} causal={causal} {'split' if use_ws else 'whole'} items")
 
 
+@pytest.mark.parametrize("B,H,Hkv,S,d,causal,scale", [
+    (1, 2, 2, 1333, 64, True, 0.125),      # ragged last query tile
+    (1, 2, 2, 1100, 64, False, -0.125),    # negative scale, ragged tail tile
+    (1, 2, 2, 1280, 64, True, 0.3),        # wide scale: split P on every tile
+    (1, 4, 2, 1280, 128, True, 128 ** -0.5),
+    (2, 3, 1, 1024, 64, False, 0.125),     # grouped K/V (3 query heads per K/V head)
+])
+def test_split_units_edge_cases(capi, B, H, Hkv, S, d, causal, scale):
+    """Shapes whose heaviest items the planner splits over two CUs (checked
+    with fa_prefill_plan_units on the device's CU count), through the C ABI
+    with the workspace: against the oracle, fp16 and fp32 outputs."""
+    import numpy as np
+
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    nb, ns = ctypes.c_int(), ctypes.c_int()
+    assert capi.fa_prefill_plan_units(B * H, S, int(causal), d, H // Hkv, cu, None, 0,
+                                      ctypes.byref(nb), ctypes.byref(ns)) == 0
+    assert ns.value > 0, "shape not split on this device"
+    g = torch.Generator().manual_seed(B * 1000 + S)
+    q = torch.randn(B, H, S, d, generator=g).half()
+    k = torch.randn(B, Hkv, S, d, generator=g).half()
+    v = torch.randn(B, Hkv, S, d, generator=g).half()
+    ref = oracle.prefill_gqa(q.numpy(), k.numpy(), v.numpy(), causal, scale)
+    ws_bytes = capi.fa_prefill_workspace_bytes(B, H, S, int(causal))
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for dtype, code in ((torch.float16, 0), (torch.float32, 1)):
+        o = torch.empty(q.shape, dtype=dtype, device="cuda")
+        rc = capi.fa_prefill_hd(p(qd), p(kd), p(vd), p(o), code, B, H, Hkv, S, d, int(causal),
+                                ctypes.c_float(scale), p(ws), ctypes.c_size_t(ws_bytes), stream)
+        assert rc == 0, capi.fa_last_error()
+        outs.append(o)
+    torch.cuda.synchronize()
+    _check(outs[0], outs[1], ref, f"split units B{B} H{H}/{Hkv} S{S} D{d} causal={causal} "
+           f"scale={scale:.3f}")
+
+
 def test_capi_decode_matches_python_api(capi):
     q, k, v, lens = (t.cuda() for t in oracle.make_decode_inputs(3, 2, 700, seed=15))
     o = torch.empty_like(q)
