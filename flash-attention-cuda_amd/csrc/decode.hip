@@ -886,13 +886,28 @@ __global__ __launch_bounds__(kBhThreads) void decode_bh_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   // Block -> position in the longest-first order. With the whole grid
   // resident (target_waves = kBhWavesPerCu x CUs), blocks [0, CUs) take one
-  // CU each and block CUs + j lands on the CU of block j: the second round
-  // takes the positions in reverse, so a CU pairs a long sequence with a
-  // short one.
+  // CU each and block CUs + j lands on the CU of block j. Of the n blocks,
+  // the 2 CUs - n longest positions run alone (on the CUs that get no second
+  // block) and the rest pair heaviest with lightest: CU j < n - CUs takes
+  // position 2 CUs - n + j, then position n - 1 - j. (Config 5: the busiest
+  // CU streams 4,541 rows against a 4,013 mean, 4,919 when every CU paired
+  // its first-round position with the reversed second round; the launch
+  // gains ~0.6 %, since the chip's HBM rate, not one CU's, sets its pace.)
   int pos = static_cast<int>(blockIdx.x);
   const int n_blocks = static_cast<int>(gridDim.x);
   const int cus = target_waves / kBhWavesPerCu;
-  if (target_waves > 0 && pos >= cus) pos = cus + (n_blocks - 1 - pos);
+  if (target_waves > 0 && n_blocks > cus) {
+    if (n_blocks <= 2 * cus) {
+      const int pairs = n_blocks - cus;  // CUs that take two blocks
+      const int singles = cus - pairs;
+      if (pos >= cus)
+        pos = n_blocks - 1 - (pos - cus);
+      else
+        pos = pos < pairs ? singles + pos : pos - pairs;
+    } else if (pos >= cus) {
+      pos = cus + (n_blocks - 1 - pos);  // three or more per CU: later rounds reversed
+    }
+  }
   int b = pos / heads;
   const int h = pos % heads;
   const bool ranked = batch <= kRankMax;
