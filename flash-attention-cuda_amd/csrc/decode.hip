@@ -1134,10 +1134,17 @@ int decode_group_chunk(int batch, int units_per_row, int max_seq, int head_dim) 
       head_dim == 128 ? GroupGeo<128>::kWavesPerCu : GroupGeo<64>::kWavesPerCu;
   const long long waves = static_cast<long long>(per_cu) * (cu > 0 ? cu : 256);
   const long long work = static_cast<long long>(max_seq) * batch * units_per_row;
-  long long rows = (work + waves - 1) / waves;
+  // head_dim 64: chunks 1.25x the one-round share, and at least 5 tiles: a
+  // wave's first tile arrives ~2 us after it starts and every chunk adds a
+  // partial to merge, so fewer, longer chunks win (measured per call: B32
+  // H14/2 L4096 ragged 15.8 -> 14.5 us, B8 H32/8 L4096 22.2 -> 19.4, B16
+  // H14/2 L2048 13.0 -> 10.1, B1 H32/8 L8192 12.1 -> 11.6, B4 H28/4 L16384
+  // 15.4 -> 15.6). head_dim 128 keeps the one-round share.
+  const bool d64 = head_dim != 128;
+  long long rows = d64 ? (5 * work + 4 * waves - 1) / (4 * waves) : (work + waves - 1) / waves;
   rows = ((rows + kGroupTile - 1) / kGroupTile) * kGroupTile;
   const long long cap = ((static_cast<long long>(max_seq) + kGroupTile - 1) / kGroupTile) * kGroupTile;
-  rows = std::max<long long>(rows, 2 * kGroupTile);
+  rows = std::max<long long>(rows, (d64 ? 5 : 2) * kGroupTile);
   return static_cast<int>(std::min(rows, std::max<long long>(cap, 2 * kGroupTile)));
 }
 
