@@ -669,6 +669,29 @@ def test_split_units_edge_cases(capi, B, H, Hkv, S, d, causal, scale):
            f"scale={scale:.3f}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_split_units_with_peaky_rows_redo_per_chunk(capi, causal):
+    """Rows 1200-1279 of a 1280-row sequence scaled x3 (their single-rounded
+    error would reach ~3e-4): the last query tiles are split over two CUs, each
+    chunk judges its own rows' rounded mass and recomputes itself with split P,
+    and the merged rows stay within the bound (fp16 and fp32 outputs)."""
+    B, H, S = 1, 2, 1280
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    nb, ns = ctypes.c_int(), ctypes.c_int()
+    assert capi.fa_prefill_plan_units(B * H, S, int(causal), 64, 1, cu, None, 0,
+                                      ctypes.byref(nb), ctypes.byref(ns)) == 0
+    assert ns.value > 0, "shape not split on this device"
+    q, k, v = oracle.make_prefill_inputs(B, H, S, seed=17)
+    q = q.float()
+    q[:, :, 1200:] *= 3.0
+    q = q.half()
+    ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, SCALE)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out32 = flashattn_cuda._prefill_fp32(qd, kd, vd, causal, SCALE)
+    out16 = flashattn_cuda.prefill(qd, kd, vd, causal, SCALE)
+    _check(out16, out32, ref, f"split units, peaky rows 1200-1279, causal={causal}")
+
+
 def test_capi_decode_matches_python_api(capi):
     q, k, v, lens = (t.cuda() for t in oracle.make_decode_inputs(3, 2, 700, seed=15))
     o = torch.empty_like(q)
