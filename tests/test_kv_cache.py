@@ -170,6 +170,74 @@ def test_graph_replayed_decode_step_matches_eager_loop(kv_heads):
     assert lens.cpu().tolist() == [prefix + steps] * B
 
 
+@pytest.mark.parametrize("kv_heads", [12, 4])
+def test_graph_of_several_steps_matches_eager_loop(kv_heads):
+    """Four append + decode steps captured in one graph (the decodes share
+    one counter slot and run back to back inside it), replayed three times
+    with the next four tokens' inputs copied in between: every output equals
+    the eager loop's."""
+    B, H, L, prefix, per_graph, replays = 2, 12, 600, 200, 4, 3
+    steps = per_graph * replays
+    qs = _rand((B, H, steps, 64), 40).cuda()
+    ks = _rand((B, kv_heads, steps, 64), 41).cuda()
+    vs = _rand((B, kv_heads, steps, 64), 42).cuda()
+    kc0 = _rand((B, kv_heads, L, 64), 43).cuda()
+    vc0 = _rand((B, kv_heads, L, 64), 44).cuda()
+    decode = flashattn_cuda.decode if kv_heads == H else flashattn_cuda.decode_gqa
+
+    kc, vc = kc0.clone(), vc0.clone()
+    lens = torch.full((B,), prefix, dtype=torch.int32, device="cuda")
+    eager = []
+    for t in range(steps):
+        flashattn_cuda.append_kv(kc, vc, ks[:, :, t:t + 1].contiguous(),
+                                 vs[:, :, t:t + 1].contiguous(), lens)
+        eager.append(decode(qs[:, :, t:t + 1].contiguous(), kc, vc, lens, SCALE).clone())
+    torch.cuda.synchronize()
+
+    kc, vc = kc0.clone(), vc0.clone()
+    lens = torch.full((B,), prefix, dtype=torch.int32, device="cuda")
+    q_in = [torch.empty(B, H, 1, 64, dtype=torch.float16, device="cuda") for _ in range(per_graph)]
+    k_in = [torch.empty(B, kv_heads, 1, 64, dtype=torch.float16, device="cuda")
+            for _ in range(per_graph)]
+    v_in = [torch.empty_like(k) for k in k_in]
+
+    def load_inputs(r):
+        for j in range(per_graph):
+            t = r * per_graph + j
+            q_in[j].copy_(qs[:, :, t:t + 1]); k_in[j].copy_(ks[:, :, t:t + 1])
+            v_in[j].copy_(vs[:, :, t:t + 1])
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kw, vw, lw = kc.clone(), vc.clone(), lens.clone()
+        load_inputs(0)
+        for j in range(per_graph):
+            flashattn_cuda.append_kv(kw, vw, k_in[j], v_in[j], lw)
+            decode(q_in[j], kw, vw, lw, SCALE)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    outs = []
+    with torch.cuda.graph(graph):
+        for j in range(per_graph):
+            flashattn_cuda.append_kv(kc, vc, k_in[j], v_in[j], lens)
+            outs.append(decode(q_in[j], kc, vc, lens, SCALE))
+    torch.cuda.synchronize()
+    assert lens.cpu().tolist() == [prefix] * B
+
+    for r in range(replays):
+        load_inputs(r)
+        graph.replay()
+        torch.cuda.synchronize()
+        for j in range(per_graph):
+            assert torch.equal(outs[j], eager[r * per_graph + j]), \
+                f"replay {r}, step {j} differs from the eager step"
+        (qs[:, :, :1].float() * 2).sum().item()
+    assert lens.cpu().tolist() == [prefix + steps] * B
+
+
 def test_capi_kv_append_matches_python_api():
     lib = ctypes.CDLL(LIB)
     lib.fa_last_error.restype = ctypes.c_char_p
