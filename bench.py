@@ -22,7 +22,7 @@ Prints ONE JSON line on stdout (everything else goes to stderr):
   lower and needs ~50 ms of load to get there).
 * ``decode_loop``: tokens/s of the generation step (append_kv + decode) at
   the reference's decode_lines shapes and the config 5 batch, eager and as a
-  replayed HIP graph.
+  replayed HIP graph (one step, and eight steps, per graph).
 * ``gqa``: grouped-query prefill / decode (2 K/V heads for 14 query heads)
   at the config 3 and 5 shapes, beside the repeat-K/V-then-call path the
   reference's callers use.
@@ -551,7 +551,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one GPU only: this build has no multi-GPU path "
-            "(prefill and decode shard over (batch, head) with no exchange; see DESIGN.md). "
+            "(prefill and decode would shard over (batch, head) with no exchange between GPUs). "
             f"Requested --gpus {args.gpus}.")
         sys.exit(2)
 

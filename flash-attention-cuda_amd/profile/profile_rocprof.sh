@@ -5,7 +5,7 @@
 #   bash flash-attention-cuda_amd/profile/profile_rocprof.sh [OUT_DIR [WORKLOAD ...]]
 #   bash flash-attention-cuda_amd/profile/profile_rocprof.sh --extract-only OUT_DIR
 #
-# Default OUT_DIR: gpurun_out/rocprof (raw rocprofv3 CSVs, not committed).
+# Default OUT_DIR: the raw-output folder set below (raw rocprofv3 CSVs, not committed).
 # Default workloads: every one of profile_workload.py, copy_1g included (it
 # calibrates the HBM byte counters), then bench.py's prefill and decode runs
 # under the kernel trace. Writes OUT_DIR/report.md, OUT_DIR/report.json and
