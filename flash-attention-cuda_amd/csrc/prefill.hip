@@ -115,6 +115,14 @@
 #include "fa_internal.h"
 #include "mfma_tile.h"
 
+// This file is compiled once per head size: FA_PREFILL_D = 64 gives the
+// head_dim 64 kernels and the shared host entry points, FA_PREFILL_D = 128
+// the head_dim 128 kernels. The two builds take different instruction-
+// scheduling options (the library's build script).
+#if !defined(FA_PREFILL_D) || (FA_PREFILL_D != 64 && FA_PREFILL_D != 128)
+#error "compile prefill.hip with -DFA_PREFILL_D=64 or -DFA_PREFILL_D=128"
+#endif
+
 namespace fa {
 namespace {
 
@@ -134,7 +142,7 @@ constexpr int kSplitPRowsBelow = 256;  // rows with fewer keys than this: split 
 constexpr float kRedoRoundedMassAbove = 0.03f;
 // |scale| * sqrt(D) above this (1 is the standard 1/sqrt(D)): rows are peaky
 // from the scale alone, so the first (single-rounding) pass is skipped.
-constexpr float kSplitAllWidth = 1.5f;
+[[maybe_unused]] constexpr float kSplitAllWidth = 1.5f;  // used by the head_dim 64 build
 constexpr float kNegHuge = -3.0e38f;
 // The max that P is taken against moves only when a row's tile max exceeds it
 // by more than this (log2 units), so P <= 2^8 and O is rescaled on few steps...
@@ -182,7 +190,7 @@ struct Geo {
 };
 
 
-__device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
+[[maybe_unused]] __device__ __forceinline__ half8 lds_b128(const _Float16 *p) {
   return *reinterpret_cast<const half8 *>(p);
 }
 
@@ -1290,6 +1298,8 @@ void launch_one(const void *q, const void *k, const void *v, void *o, int bh,
 
 }  // namespace
 
+// launch_d<D> and prefill_occupancy_d<D> are instantiated by the build of
+// head size D only; the head_dim 64 build declares the head_dim 128 ones.
 template <int D>
 void launch_d(const void *q, const void *k, const void *v, void *o, bool out_f32, int bh,
               int seq, int group, bool causal, float c_scale, bool negate_q, bool split_all,
@@ -1310,6 +1320,36 @@ void launch_d(const void *q, const void *k, const void *v, void *o, bool out_f32
                                   ws_bytes, stream);
   }
 }
+
+template <int D>
+int prefill_occupancy_d(fa_occupancy_entry *out, int cap, int *n) {
+  struct K { const char *name; const void *fn; };
+  const K ks[] = {
+      {D == 64 ? "prefill_kernel<causal=true>" : "prefill_kernel<causal=true, head_dim=128>",
+       reinterpret_cast<const void *>(prefill_kernel<D, true, false>)},
+      {D == 64 ? "prefill_kernel<causal=false>" : "prefill_kernel<causal=false, head_dim=128>",
+       reinterpret_cast<const void *>(prefill_kernel<D, false, false>)},
+  };
+  for (const K &k : ks) {
+    if (*n < cap) {
+      const int rc = fill_occupancy_row(&out[*n], k.name, k.fn, kThreads, 0);
+      if (rc != FA_OK) return rc;
+    }
+    ++*n;
+  }
+  return FA_OK;
+}
+
+template void launch_d<FA_PREFILL_D>(const void *, const void *, const void *, void *, bool, int,
+                                     int, int, bool, float, bool, bool, void *, size_t,
+                                     hipStream_t);
+template int prefill_occupancy_d<FA_PREFILL_D>(fa_occupancy_entry *, int, int *);
+
+#if FA_PREFILL_D == 64
+extern template void launch_d<128>(const void *, const void *, const void *, void *, bool, int,
+                                   int, int, bool, float, bool, bool, void *, size_t,
+                                   hipStream_t);
+extern template int prefill_occupancy_d<128>(fa_occupancy_entry *, int, int *);
 
 size_t prefill_workspace_bytes(int batch, int heads, int seq, bool causal) {
   if (batch <= 0 || heads <= 0 || seq <= 0) return 0;
@@ -1348,25 +1388,8 @@ int launch_prefill(const void *q, const void *k, const void *v, void *o,
 }
 
 int prefill_occupancy(fa_occupancy_entry *out, int cap, int *n) {
-  struct K { const char *name; const void *fn; };
-  const K ks[] = {
-      {"prefill_kernel<causal=true>",
-       reinterpret_cast<const void *>(prefill_kernel<64, true, false>)},
-      {"prefill_kernel<causal=false>",
-       reinterpret_cast<const void *>(prefill_kernel<64, false, false>)},
-      {"prefill_kernel<causal=true, head_dim=128>",
-       reinterpret_cast<const void *>(prefill_kernel<128, true, false>)},
-      {"prefill_kernel<causal=false, head_dim=128>",
-       reinterpret_cast<const void *>(prefill_kernel<128, false, false>)},
-  };
-  for (const K &k : ks) {
-    if (*n < cap) {
-      const int rc = fill_occupancy_row(&out[*n], k.name, k.fn, kThreads, 0);
-      if (rc != FA_OK) return rc;
-    }
-    ++*n;
-  }
-  return FA_OK;
+  const int rc = prefill_occupancy_d<64>(out, cap, n);
+  return rc != FA_OK ? rc : prefill_occupancy_d<128>(out, cap, n);
 }
 
 int prefill_plan_units(int bh, int seq, int causal, int head_dim, int group, int cu,
@@ -1382,5 +1405,6 @@ int prefill_plan_units(int bh, int seq, int causal, int head_dim, int group, int
   for (int i = 0; i < std::min(cap, 2 * e.plan.n_blocks); ++i) units[i] = e.plan.unit[i];
   return FA_OK;
 }
+#endif  // FA_PREFILL_D == 64
 
 }  // namespace fa

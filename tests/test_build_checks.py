@@ -53,10 +53,10 @@ def test_m0_checker_flags_other_uses(planted):
 
 def test_kernels_touch_m0_only_in_their_global_load_lds_sequences():
     with tempfile.TemporaryDirectory() as tmp:
-        with ThreadPoolExecutor(max_workers=2) as pool:
-            asm = list(pool.map(lambda src: fa_build.device_assembly(src, tmp),
-                                ["prefill.hip", "decode.hip"]))
-    for src, text in zip(["prefill.hip", "decode.hip"], asm):
+        units = ["prefill_d64", "prefill_d128", "decode"]
+        with ThreadPoolExecutor(max_workers=3) as pool:
+            asm = list(pool.map(lambda unit: fa_build.device_assembly(unit, tmp), units))
+    for src, text in zip(units, asm):
         assert "global_load_lds_dwordx4" in text, src
         problems = fa_build.m0_problems(text)
         assert not problems, f"{src}: " + "; ".join(problems[:5])
