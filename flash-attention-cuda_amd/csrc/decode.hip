@@ -583,8 +583,11 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(
 //                 columns (columns past the group compute zeros, unused);
 //   softmax       per lane: one query column, 16 of the 32 rows (the other 16
 //                 in lane l ^ 32), log2 domain, rows past the chunk -> -inf;
-//   O^T += V^T P^T with P split into fp16 hi + lo parts (4 + 4 MFMAs), so the
-//                 weights keep fp32 accuracy whatever the number of rows.
+//   O^T += V^T P^T with P rounded once to fp16 (4 MFMAs) on chunks of
+//                 sequences of >= 256 rows, split into fp16 hi + lo parts
+//                 (4 + 4 MFMAs, fp32 accuracy) otherwise; a chunk whose
+//                 single-rounded weights carry too much rounded mass (below)
+//                 is computed again with split P.
 // K and V tiles stream through a per-wave LDS ring filled by direct
 // global->LDS loads kGroupAhead tiles ahead (row-major, 16-byte chunks
 // XOR-swizzled, as the prefill kernel's tiles). A block is one wave, so
@@ -612,6 +615,11 @@ struct GroupGeo {
 };
 
 constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
+// A chunk is computed again with split P when, for one of its queries, the
+// squares of its single-rounded weights sum to more than this fraction of
+// the squared row sum (the prefill's rule: one fp16 rounding of each weight
+// moves the output by about 1.5e-3 sqrt(r / l^2)).
+constexpr float kGroupRedoMassAbove = 0.03f;
 // Wide logits, |scale| sqrt(D) > 1.5, in the log2 domain of qscale.
 constexpr float kGroupWideLog2 = 1.5f * kLog2e;
 
@@ -619,10 +627,13 @@ constexpr float kGroupWideLog2 = 1.5f * kLog2e;
 // `sacc`: m is the running max in the log2 domain (scores times c), l this
 // lane's share of the row sum. MASK: rows >= lim of this lane's half are past
 // the chunk end. SPLIT: P as fp16 hi + lo (two PV products) instead of one
-// fp16 rounding; l sums the same fp16 values the products consume.
+// fp16 rounding; l sums the same fp16 values the products consume. Without
+// SPLIT, r (this lane's share of the rounded mass, in units of m) adds the
+// squares of the rounded weights, less the exact 1 of a tile whose largest
+// weight is exactly 1 (the key at m; half in each lane of the pair).
 template <int D, bool MASK, bool SPLIT>
 __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&vf)[2][D / 32],
-                                                 int lim, float c, float &m, float &l,
+                                                 int lim, float c, float &m, float &l, float &r,
                                                  floatx16 (&o)[D / 32]) {
   float mx = -INFINITY;
 #pragma unroll
@@ -631,12 +642,18 @@ __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&v
     mx = fmaxf(mx, sacc[a]);
   }
   mx = max_lane_pair(mx);  // the tile has a row in range: finite
-  const float m_new = fmaxf(m, mx * c);
+  float mx_c;
+  {
+    // Rounded once: a tile that sets m gets largest weight exp2(0) = 1.
+#pragma clang fp contract(off)
+    mx_c = mx * c;
+  }
+  const float m_new = fmaxf(m, mx_c);
   const float alpha = fast_exp2(m - m_new);
   m = m_new;
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   half8 p_hi[2], p_lo[2];
-  float lsum = 0.f;
+  float lsum = 0.f, sq = 0.f;
 #pragma unroll
   for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
@@ -658,9 +675,12 @@ __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&v
         p_lo[hs][e] = lo2[0];
         p_lo[hs][e + 1] = lo2[1];
         lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
+      } else {
+        sq = __builtin_amdgcn_fdot2(hi2, hi2, sq, false);
       }
     }
   l = fmaf(l, alpha, lsum);
+  if (!SPLIT) r = r * (alpha * alpha) + (sq - (mx_c == m_new ? 0.5f : 0.0f));
   // alpha is exactly 1 wherever the max did not rise (wave-uniform branch).
   if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
@@ -762,7 +782,7 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     if (t < n_tiles) issue(t);
 
   const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
-  float m = kNegBig, l = 0.f;
+  float m = kNegBig, l = 0.f, r = 0.f;
   floatx16 o[kDB];
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
@@ -819,17 +839,36 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
       if (partial_tail && t == n_tiles - 1) {
         // Element a: row 8 (a / 4) + 4 g + a % 4 of the tile.
         const int lim = end - (begin + t * kGroupTile) - 4 * g;
-        group_softmax_pv<D, true, SPLIT>(sacc, vf, lim, c_scale, m, l, o);
+        group_softmax_pv<D, true, SPLIT>(sacc, vf, lim, c_scale, m, l, r, o);
       } else {
-        group_softmax_pv<D, false, SPLIT>(sacc, vf, 0, c_scale, m, l, o);
+        group_softmax_pv<D, false, SPLIT>(sacc, vf, 0, c_scale, m, l, r, o);
       }
     }
   };
   const bool wide = qscale * qscale * static_cast<float>(D) > kGroupWideLog2 * kGroupWideLog2;
-  if (len < kGroupSplitPBelow || wide)
+  if (len < kGroupSplitPBelow || wide) {
     run(std::true_type{});
-  else
+  } else {
     run(std::false_type{});
+    // A query of the unit whose row a few keys carry (beyond its exact P = 1
+    // key) has a large r / l^2: the chunk is computed again with split P.
+    // Every load of the ring has been consumed, so it restarts from tile 0.
+    const float l_row = l + __shfl_xor(l, 32);
+    const float r_row = r + __shfl_xor(r, 32);
+    const bool peaky = col < nq && r_row > kGroupRedoMassAbove * l_row * l_row;
+    if (__builtin_amdgcn_ballot_w64(peaky) != 0) {
+      m = kNegBig;
+      l = 0.f;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) o[db][a] = 0.f;
+#pragma unroll
+      for (int t = 0; t < kGroupAhead; ++t)
+        if (t < n_tiles) issue(t);
+      run(std::true_type{});
+    }
+  }
 
   // Lanes l and l ^ 32 hold the two row halves of column col: m is shared,
   // l adds up; each lane writes its half of the D head dims.
