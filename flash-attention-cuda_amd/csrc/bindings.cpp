@@ -27,6 +27,7 @@
 
 #include <cmath>
 #include <string>
+#include <vector>
 
 #include "flashattn_hip.h"
 
@@ -284,11 +285,13 @@ void append_kv(const at::Tensor &k_cache, const at::Tensor &v_cache, const at::T
 
 // bindings.cpp:80-97.
 py::list occupancy_report() {
-  fa_occupancy_entry rows[16];
+  // The first call counts the rows, the second fills them.
   int n = 0;
-  check_status(fa_occupancy_report(rows, 16, &n));
+  check_status(fa_occupancy_report(nullptr, 0, &n));
+  std::vector<fa_occupancy_entry> rows(static_cast<size_t>(n));
+  check_status(fa_occupancy_report(rows.data(), n, &n));
   py::list out;
-  for (int i = 0; i < n && i < 16; ++i) {
+  for (int i = 0; i < n && i < static_cast<int>(rows.size()); ++i) {
     py::dict row;
     row["kernel"] = std::string(rows[i].kernel);
     row["threads_per_block"] = rows[i].threads_per_block;
