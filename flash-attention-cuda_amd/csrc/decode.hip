@@ -1121,17 +1121,34 @@ int group_queries(int group) {
 }  // namespace
 
 // Counter slot of g_merge_counters for the current device and `stream`,
-// claimed on first use and kept; nullptr (decode: the two-launch path) when
-// n_bh counters exceed a slot or every slot is taken. The split-K decode and
-// the split prefill units share a stream's slot: kernels on one stream run
-// one at a time, and each leaves its counters at zero.
+// claimed on first use and kept; nullptr (decode: the two-launch path;
+// prefill: whole items) when n_bh counters exceed a slot or every slot is
+// taken. The split-K decode and the split prefill units share a stream's
+// slot: kernels on one stream run one at a time, and each leaves its
+// counters at zero.
+//  * hipStreamPerThread names a different stream in every thread and
+//    hipStreamLegacy the legacy default stream: one handle, several streams,
+//    so neither gets a slot.
+//  * A stream under graph capture gets a slot of that capture's own (keyed by
+//    its capture id): graphs captured one after another on one stream (as
+//    torch.cuda.graph does) hold different slots and may replay concurrently.
+//    Replays of one graph share its slot and must not overlap each other.
 unsigned *merge_counters(hipStream_t stream, size_t n_bh) {
   if (n_bh > static_cast<size_t>(kCountersPerSlot)) return nullptr;
+  if (stream == hipStreamPerThread || stream == hipStreamLegacy) return nullptr;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  unsigned long long capture = 0;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamGetCaptureInfo(stream, &status, &capture) != hipSuccess) {
+    (void)hipGetLastError();  // the query's error is not the caller's
+    return nullptr;
+  }
+  if (status != hipStreamCaptureStatusActive) capture = 0;
   struct Owner {
     int dev;
     hipStream_t stream;
+    unsigned long long capture;
   };
   static std::mutex mu;
   static unsigned *base[kMaxDevices];
@@ -1147,10 +1164,10 @@ unsigned *merge_counters(hipStream_t stream, size_t n_bh) {
   }
   if (base[dev] == nullptr) return nullptr;
   for (int i = 0; i < n_used; ++i)
-    if (owner[i].dev == dev && owner[i].stream == stream)
+    if (owner[i].dev == dev && owner[i].stream == stream && owner[i].capture == capture)
       return base[dev] + static_cast<size_t>(i) * kCountersPerSlot;
   if (n_used == kCounterSlots) return nullptr;
-  owner[n_used] = {dev, stream};
+  owner[n_used] = {dev, stream, capture};
   return base[dev] + static_cast<size_t>(n_used++) * kCountersPerSlot;
 }
 
@@ -1347,7 +1364,14 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
 
 int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
   struct K { const char *name; const void *fn; int threads; };
+  // The split-K path runs decode_split_fused_kernel (4 waves per block for
+  // chunks of <= 256 rows, else 2); decode_split_kernel + decode_merge_kernel
+  // serve it when no counter slot is free.
   const K ks[] = {
+      {"decode_split_fused_kernel<waves=4>",
+       reinterpret_cast<const void *>(decode_split_fused_kernel<64, false, 4>), 4 * kWave},
+      {"decode_split_fused_kernel<waves=2>",
+       reinterpret_cast<const void *>(decode_split_fused_kernel<64, false, 2>), 2 * kWave},
       {"decode_split_kernel", reinterpret_cast<const void *>(decode_split_kernel<64>),
        kSplitThreads},
       {"decode_merge_kernel",
@@ -1355,6 +1379,10 @@ int decode_occupancy(fa_occupancy_entry *out, int cap, int *n) {
       {"decode_bh_kernel", reinterpret_cast<const void *>(decode_bh_kernel<64, false>),
        kBhThreads},
       {"decode_group_kernel", reinterpret_cast<const void *>(decode_group_kernel<64>), kWave},
+      {"decode_split_fused_kernel<head_dim=128, waves=4>",
+       reinterpret_cast<const void *>(decode_split_fused_kernel<128, false, 4>), 4 * kWave},
+      {"decode_split_fused_kernel<head_dim=128, waves=2>",
+       reinterpret_cast<const void *>(decode_split_fused_kernel<128, false, 2>), 2 * kWave},
       {"decode_split_kernel<head_dim=128>",
        reinterpret_cast<const void *>(decode_split_kernel<128>), kSplitThreads},
       {"decode_merge_kernel<head_dim=128>",

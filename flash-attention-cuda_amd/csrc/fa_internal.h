@@ -63,9 +63,11 @@ int launch_decode(const void *q, const void *k_cache, const void *v_cache,
 // B * H >= CUs or a short cache) merges in LDS and needs none.
 bool decode_needs_workspace(int batch, int heads, int kv_heads, int max_seq);
 // Counter slot (kMergeCountersPerSlot zeroed counters) of the current device
-// for kernels launched on `stream`, claimed on first use and kept; nullptr
-// when `n` counters exceed a slot or every slot is taken. Kernels that count
-// arrivals in it set each counter back to zero before they end (decode.hip).
+// for kernels launched on `stream` (and, under graph capture, that capture),
+// claimed on first use and kept; nullptr when `n` counters exceed a slot,
+// every slot is taken, or `stream` is hipStreamPerThread / hipStreamLegacy.
+// Kernels that count arrivals in it set each counter back to zero before
+// they end (decode.hip).
 constexpr size_t kMergeCountersPerSlot = 4096;
 unsigned *merge_counters(hipStream_t stream, size_t n);
 // Decode work units per batch row: one per head without grouped queries,

@@ -466,6 +466,92 @@ def test_decode_split_path_agrees_across_many_streams():
         assert (got - want).abs().max().item() <= 1e-6
 
 
+def test_decode_split_path_on_per_thread_streams(capi):
+    """hipStreamPerThread is one handle that names a different stream in each
+    thread, so it gets no counter slot: two threads decoding on it at once
+    (C ABI, fp32 outputs, each its own inputs and workspace) match decodes of
+    the same inputs on the default stream."""
+    import threading
+
+    per_thread = ctypes.c_void_p(2)  # hipStreamPerThread
+    batch, heads, max_seq = 1, 12, 4096
+    ws_bytes = capi.fa_decode_workspace_bytes(batch, heads, max_seq, 0)
+    assert ws_bytes > 0  # the split-K shape
+    cases = []
+    for t in range(2):
+        q, k, v, lens = oracle.make_decode_inputs(batch, heads, max_seq, seed=40 + t)
+        qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+        want = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE)
+        outs = [torch.empty(batch, heads, 1, 64, dtype=torch.float32, device="cuda")
+                for _ in range(16)]
+        ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device="cuda")
+        cases.append((qd, kd, vd, ld, want, outs, ws))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(case):
+        qd, kd, vd, ld, _, outs, ws = case
+        for o in outs:
+            rc = capi.fa_decode(ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(kd.data_ptr()),
+                                ctypes.c_void_p(vd.data_ptr()), ctypes.c_void_p(ld.data_ptr()),
+                                ctypes.c_void_p(o.data_ptr()), 1, batch, heads, max_seq,
+                                ctypes.c_float(SCALE), 0, ctypes.c_void_p(ws.data_ptr()),
+                                ctypes.c_size_t(ws_bytes), per_thread)
+            if rc != 0:
+                errors.append(capi.fa_last_error())
+
+    threads = [threading.Thread(target=worker, args=(c,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()  # every stream, the per-thread ones included
+    assert not errors, errors
+    for qd, kd, vd, ld, want, outs, ws in cases:
+        for o in outs:
+            assert (o - want).abs().max().item() <= 1e-6
+
+
+def test_split_decode_graphs_captured_on_one_stream_replay_concurrently():
+    """torch.cuda.graph captures every graph on one capture stream; a graph
+    holding the single-launch split-K decode keeps a counter slot of its own
+    capture, so two such graphs replayed at once on two streams both give
+    their eager results (checked on every replay, with eager work and a
+    synchronisation between rounds)."""
+    graphs, outs, wants, inputs = [], [], [], []
+    for t in range(2):
+        q, k, v, lens = oracle.make_decode_inputs(1, 12, 4096, seed=50 + t)
+        qd, kd, vd, ld = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+        inputs.append((qd, kd, vd, ld))
+        want = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+        flashattn_cuda.decode(qd, kd, vd, ld, SCALE)  # warm-up outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = flashattn_cuda.decode(qd, kd, vd, ld, SCALE)
+        torch.cuda.synchronize()
+        graphs.append(g)
+        outs.append(out)
+        wants.append(want)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for rnd in range(4):
+        for o in outs:
+            o.zero_()
+        s1.wait_stream(torch.cuda.current_stream())
+        s2.wait_stream(torch.cuda.current_stream())
+        for _ in range(3):
+            with torch.cuda.stream(s1):
+                graphs[0].replay()
+            with torch.cuda.stream(s2):
+                graphs[1].replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outs, wants):
+            assert torch.equal(o, w), f"round {rnd}"
+        eager = flashattn_cuda.decode(*inputs[rnd % 2], SCALE)  # eager work between rounds
+        torch.cuda.synchronize()
+        assert torch.equal(eager, wants[rnd % 2])
+
+
 def test_decode_whole_sequence_split_invariance_fp32():
     q, k, v, lens = oracle.make_decode_inputs(32, 10, 1500, seed=22,
                                               lens=_ragged_lens(32, 1500, seed=23))
@@ -559,8 +645,12 @@ def test_occupancy_report_rows():
     assert names == ["prefill_kernel<causal=true>", "prefill_kernel<causal=false>",
                      "prefill_kernel<causal=true, head_dim=128>",
                      "prefill_kernel<causal=false, head_dim=128>",
+                     "decode_split_fused_kernel<waves=4>", "decode_split_fused_kernel<waves=2>",
                      "decode_split_kernel", "decode_merge_kernel", "decode_bh_kernel",
-                     "decode_group_kernel", "decode_split_kernel<head_dim=128>",
+                     "decode_group_kernel",
+                     "decode_split_fused_kernel<head_dim=128, waves=4>",
+                     "decode_split_fused_kernel<head_dim=128, waves=2>",
+                     "decode_split_kernel<head_dim=128>",
                      "decode_merge_kernel<head_dim=128>", "decode_bh_kernel<head_dim=128>",
                      "decode_group_kernel<head_dim=128>"]
     for r in rows:
