@@ -196,6 +196,11 @@ int prefill_impl(const void *q, const void *k, const void *v, void *o, int out_d
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return set_error(FA_ERR_INVALID_ARGUMENT,
                      "q, k, v and o must be 16-byte aligned device pointers");
+  // The split units store their partials with coherent (atomic) stores; the
+  // workspace takes the decode workspace's 16-byte rule.
+  if (workspace != nullptr && !aligned16(workspace))
+    return set_error(FA_ERR_INVALID_ARGUMENT,
+                     "workspace must be a 16-byte aligned device pointer (or NULL)");
   if (out_dtype != FA_OUT_F16 && out_dtype != FA_OUT_F32)
     return set_error(FA_ERR_INVALID_ARGUMENT, "unknown out_dtype %d", out_dtype);
   if (batch <= 0 || heads <= 0)

@@ -115,6 +115,9 @@ def test_prefill_rejects_bad_arguments_before_any_launch(lib):
     assert rc == FA_ERR_INVALID_ARGUMENT and b"scale must be finite" in lib.fa_last_error()
     rc = lib.fa_prefill(p, p, p, p, 7, 1, 1, 8, 1, f(0.125), None, ctypes.c_size_t(0), None)
     assert rc == FA_ERR_INVALID_ARGUMENT and b"out_dtype" in lib.fa_last_error()
+    # A workspace that is not 16-byte aligned is refused before anything runs.
+    rc = lib.fa_prefill(p, p, p, p, 0, 1, 1, 8, 1, f(0.125), odd, ctypes.c_size_t(32), None)
+    assert rc == FA_ERR_INVALID_ARGUMENT and b"workspace must be" in lib.fa_last_error()
 
 
 def test_decode_rejects_bad_arguments_before_any_launch(lib):

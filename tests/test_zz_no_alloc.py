@@ -107,3 +107,50 @@ def test_noalloc_decode_refuses_shapes_beyond_its_scratch(lib):
                                   b, h, h, lmax, d, ctypes.c_float(0.125), 0, stream)
     assert rc == FA_ERR_WORKSPACE
     assert b"noalloc" in lib.fa_last_error()
+
+
+_CAPTURE_FIRST_CALL = r"""
+import ctypes, sys, torch
+lib = ctypes.CDLL(sys.argv[1])
+lib.fa_last_error.restype = ctypes.c_char_p
+g = torch.Generator().manual_seed(91)
+b, h, hkv, lmax, d = 1, 8, 2, 1700, 64
+q = torch.randn(b, h, 1, d, generator=g).half().cuda()
+k = torch.randn(b, hkv, lmax, d, generator=g).half().cuda()
+v = torch.randn(b, hkv, lmax, d, generator=g).half().cuda()
+lens = torch.tensor([lmax], dtype=torch.int32).cuda()
+o = torch.empty(b, h, 1, d, dtype=torch.float32, device="cuda")
+ref = torch.empty_like(o)
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+def call(out):
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return lib.fa_decode_hd_noalloc(P(q), P(k), P(v), P(lens), P(out), 1, b, h, hkv, lmax, d,
+                                    ctypes.c_float(d ** -0.5), 0, s)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    rc = call(o)  # the process's first call into the library
+assert rc == 0, lib.fa_last_error()
+torch.cuda.synchronize()
+for r in range(4):
+    o.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert call(ref) == 0, lib.fa_last_error()  # eager work between replays
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref), f"replay {r}"
+print("ok")
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """A fresh process whose first library call is fa_decode_hd_noalloc
+    inside torch.cuda.graph (the scratch array and the counter slot are
+    looked up during the capture): every replay equals the eager call."""
+    import subprocess
+    import sys
+
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST_CALL, LIB], capture_output=True,
+                         text=True, timeout=300)
+    print(res.stdout, res.stderr[-2000:])
+    assert res.returncode == 0 and "ok" in res.stdout
