@@ -5,8 +5,10 @@
     python profile_workload.py list            # print the workload table as JSON
 
 Each workload builds its inputs on the CPU from a fixed seed (the recipe of
-the benchmark), moves them to the GPU, runs 0.1 s of untimed launches (the GPU
-reaches its sustained clock), then 5 warm-up and ITERS profiled calls. It is
+the benchmark), moves them to the GPU (enough copies, rotated call by call,
+that their total exceeds twice the 256 MB MALL, as bench.py's per-config
+sweep does), runs 0.1 s of untimed launches (the GPU reaches its sustained
+clock), then 5 warm-up and ITERS profiled calls. It is
 the counterpart of the reference's bench/profile_workload.py (prefill and
 decode workloads for its Nsight captures), over this build's BASELINE configs.
 
@@ -86,7 +88,11 @@ def _prefill(batch, heads, seq, causal, d=64):
     g = torch.Generator().manual_seed(0)
     shape = (batch, heads, seq, d)
     q, k, v = (torch.randn(shape, generator=g).half().cuda() for _ in range(3))
-    _run([lambda: fa.prefill(q, k, v, causal, d ** -0.5)])  # 0.125 = SCALE at d = 64
+    # Rotate input copies through more than 2x the MALL, as bench.py's
+    # per-config sweep (the reference protocol) does.
+    n = _copies(3 * q.numel() * 2)
+    sets = [(q, k, v)] + [tuple(t.clone() for t in (q, k, v)) for _ in range(n - 1)]
+    _run([lambda s=s: fa.prefill(s[0], s[1], s[2], causal, d ** -0.5) for s in sets])
 
 
 def _decode_inputs(batch, heads, lmax, lens=None, d=64):
