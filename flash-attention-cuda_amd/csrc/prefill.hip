@@ -81,16 +81,13 @@
 // head_dim 64 on the matrix cores (one v_mfma_f32_16x16x32_f16 per 16-key
 // step against a 0/1 selector, rowsum_mfma), at head_dim 128 per lane with
 // v_dot2_f32_f16.
-// The max m: rows that see >= 1024 keys take m from the exact max of their
-// half's first tile and keep it through the pipelined steps, which compute
-// no tile max at all (no max reduction, no decision, no rescale); a key that
-// later weighs 2^16 or more overflows its fp16 P, the row sum turns
-// non-finite, and the block is computed again with split P. Their masked
-// last step takes a lazy max: m moves, to the row's running max, only when
-// the tile max exceeds it by more than 8 (log2 units) or carries more than
-// 1/16 of the row sum so far. Shorter rows keep m at the exact running max
-// (every step where some row's max rose rescales). Whenever a tile sets m,
-// its dominant key enters the PV product as P = 1 exactly.
+// The max m: rows that see >= 1024 keys take a lazy max. m moves, to the
+// row's exact running max, only when a tile max exceeds it by more than 8
+// (log2 units), so P <= 2^8, or when the new max carries more than 1/16 of
+// the row sum so far; O is then rescaled on a few steps per item instead of
+// on most of them. Shorter rows keep m at the exact running max (every step
+// where some row's max rose rescales). Whenever a tile sets m, its dominant
+// key enters the PV product as P = 1 exactly.
 //
 // Precision of P: one fp16 rounding of each weight w = p / l moves an output
 // row by about 2^-11 sqrt(sum w^2) times the spread of V, summed over the
@@ -382,19 +379,6 @@ __device__ __forceinline__ void tile_exp(const floatx16 (&s)[Geo<D>::kKB], float
   }
   if constexpr (!kMfmaRowSum<D>) st.l += lsum;
   if (!SPLIT) st.r += sq - (pm == 1.0f ? 0.5f : 0.0f);
-}
-
-// The pipelined steps of rows that see >= kLazyMaxRowsFrom keys take no tile
-// max: m stays where the half's first tile put it (that tile's exact row
-// max), so P needs no max reduction, no decision and no rescale. A later key may then weigh more than 1; one that
-// weighs 2^16 or more overflows its fp16 P, which makes the row sum
-// non-finite and sends the block to the split-P pass (the verdict below).
-// alpha = 1 and a largest weight that is not exactly 1 (no key of these
-// tiles leaves the rounded mass).
-__device__ __forceinline__ bool fixed_max(float &alpha, float &pm) {
-  alpha = 1.0f;
-  pm = 0.0f;
-  return false;
 }
 
 // O (and, head_dim 64, the row sum on the matrix cores) follow a move of m
@@ -715,10 +699,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   // exact running max, whose P = 1 key takes no rounding.
   const float slack =
       (CAUSAL ? q0 : seq) >= kLazyMaxRowsFrom ? kLazyMaxSlack : 0.f;
-  // The same rows keep m fixed through the pipelined steps (fixed_max); the
-  // shorter ones take the exact max of every tile, whose P = 1 keys leave
-  // their rounded mass (otherwise rows of a few hundred keys redo blocks).
-  const bool fixed = slack > 0.f;
 
   half8 qf[kDS];
   SoftmaxState<D> st;
@@ -870,8 +850,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       ring.advance(kk);
       note_row_sum(st);
       rescale_o(st, alpha, rescale);
-      rescale = fixed ? fixed_max(alpha, pm_b)
-                      : tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
+      rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
       rowsum_mfma<D>(sel, p_a, st.lacc);
       qk_mfma(kf, qf, s_a);
       pv_mfma(vf, p_a, st.o);
@@ -884,8 +863,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       ring.advance(kk + 1);
       note_row_sum(st);
       rescale_o(st, alpha, rescale);
-      rescale = fixed ? fixed_max(alpha, pm_a)
-                      : tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
+      rescale = tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
       rowsum_mfma<D>(sel, p_b, st.lacc);
       qk_mfma(kf, qf, s_b);
       pv_mfma(vf, p_b, st.o);
@@ -907,8 +885,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       ring.advance(kk);
       note_row_sum(st);
       rescale_o(st, alpha, rescale);
-      rescale = fixed ? fixed_max(alpha, pm_b)
-                      : tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
+      rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
       if (tail) qk_mfma(kf, qf, s_a);
       rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
@@ -956,9 +933,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     if (half == 0) {
       const float l_row = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
       const float r_row = st.r + __shfl_xor(st.r, 32);
-      // A row sum that is not finite: some P overflowed fp16 (see fixed_max).
-      const bool peaky = my_q < seq && (!(l_row < INFINITY) ||
-                                        r_row > kRedoRoundedMassAbove * l_row * l_row);
+      const bool peaky = my_q < seq && r_row > kRedoRoundedMassAbove * l_row * l_row;
       const float verdict = __builtin_amdgcn_ballot_w64(peaky) != 0 ? 1.0f : 0.0f;
       if (lane == 0) xchg[0] = verdict;
     }

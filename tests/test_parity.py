@@ -341,12 +341,11 @@ def test_lazy_max_late_rise_and_slow_drift(d, causal):
 
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-def test_fixed_max_overflow_takes_the_split_pass(d, causal):
-    """Rows of >= 1024 keys keep their first tile's max through the pipelined
-    steps. One key (row 1700) scaled x8 weighs up to ~2^40 against that max in
-    the rows whose dot product with it is large, so its fp16 P overflows; the
-    row sum turns non-finite and those blocks are computed again with split
-    P. Every row still matches the oracle."""
+def test_one_late_key_far_above_the_running_max(d, causal):
+    """One key (row 1700) scaled x8 sits up to ~2^40 above the running max of
+    the rows whose dot product with it is large, late in rows of >= 1024 keys
+    (the lazy max): m must move onto it, or its fp16 P overflows. Every row
+    still matches the oracle."""
     seq = 2048
     scale = d ** -0.5
     q, k, v = oracle.make_prefill_inputs(1, 2, seq, seed=68, head_dim=d)
@@ -356,7 +355,7 @@ def test_fixed_max_overflow_takes_the_split_pass(d, causal):
     ref = oracle.prefill(q.numpy(), k.numpy(), v.numpy(), causal, scale)
     out32 = flashattn_cuda._prefill_fp32(q.cuda(), k.cuda(), v.cuda(), causal, scale)
     out16 = flashattn_cuda.prefill(q.cuda(), k.cuda(), v.cuda(), causal, scale)
-    _check(out16, out32, ref, f"overflowing P under the fixed max D{d} causal={causal}")
+    _check(out16, out32, ref, f"late dominant key D{d} causal={causal}")
 
 
 def test_decode_equals_prefill_rows_at_full_size():
