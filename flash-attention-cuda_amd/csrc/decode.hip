@@ -119,6 +119,28 @@ __device__ __forceinline__ void load_slots(RowSlotsT<G> &r, const _Float16 *kp,
   }
 }
 
+// Keeps a load that only later code uses from being sunk below a branch
+// between the two: each early exit "uses" the loaded value (it waits for the
+// load there), so the load stays where it was written, ahead of the branch.
+template <typename T, int N>
+__device__ __forceinline__ void hold(const T (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" ::"v"(x[i]));
+}
+
+// Rows at or past `end` of slots loaded from row0 with a larger bound (they
+// may hold any bits, NaN included, which a zero weight would not cancel).
+template <int D, int G>
+__device__ __forceinline__ void zero_rows_from(RowSlotsT<G> &r, int row0, int end, int sub) {
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    if (row0 + u * RowGeo<D>::kRowsPerGroup + sub >= end) {
+      r.k[u] = make_uint4(0, 0, 0, 0);
+      r.v[u] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
 __device__ __forceinline__ void unpack8(const uint4 &raw, float f[8]) {
   const half2 *h = reinterpret_cast<const half2 *>(&raw);
 #pragma unroll
@@ -394,8 +416,26 @@ __global__ __launch_bounds__(W * kWave) void decode_split_fused_kernel(
   const int bh = static_cast<int>(blockIdx.x) / n_groups;
   const int g = static_cast<int>(blockIdx.x) % n_groups;
   const int b = bh / heads;
+  const int sub = lane / RowGeo<D>::kLanesPerRow;
+  const int slice = lane % RowGeo<D>::kLanesPerRow;
+  const int begin = (g * W + wave) * chunk;
+  const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
+  const _Float16 *kp = k_cache + head_off;
+  const _Float16 *vp = v_cache + head_off;
+  // The query and the chunk's first sub-step are requested together with
+  // seq_lens (one memory round trip before the rows arrive, not two): the
+  // chunk start does not depend on the length, and rows below max_seq lie
+  // in the cache. Rows at or past the length are zeroed once it is known.
+  constexpr int kStepRows = RowGeo<D>::kRowsPerGroup * kGroupsPerStep;
+  // (The row loads are predicated per lane, which keeps the compiler from
+  // sinking them below the length tests; the query load is held there.)
+  RowSlotsT<kGroupsPerStep> cur, nxt;
+  load_slots<D>(cur, kp, vp, begin, min(max_seq, begin + chunk), sub, slice);
+  half2 qh[4];
+  load_query<D>(q, bh, slice, qh);
   const int len = min(seq_lens[b], max_seq);
   if (len <= 0) {
+    hold(qh);
     // decode.cu:172: a sequence with no rows gets a zero output.
     if (g == 0 && wave == 0) {
 #pragma unroll
@@ -411,25 +451,18 @@ __global__ __launch_bounds__(W * kWave) void decode_split_fused_kernel(
   }
   const int group_rows = W * chunk;
   const int n_live = (len + group_rows - 1) / group_rows;  // groups with rows
-  if (g >= n_live) return;
+  if (g >= n_live) {
+    hold(qh);
+    return;
+  }
 
-  const int sub = lane / RowGeo<D>::kLanesPerRow;
-  const int slice = lane % RowGeo<D>::kLanesPerRow;
   float m = kNegBig, l = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  const int begin = (g * W + wave) * chunk;
   if (begin < len) {
     const int end = min(len, begin + chunk);
-    const size_t head_off = static_cast<size_t>(bh) * max_seq * D;
-    const _Float16 *kp = k_cache + head_off;
-    const _Float16 *vp = v_cache + head_off;
-    constexpr int kStepRows = RowGeo<D>::kRowsPerGroup * kGroupsPerStep;
-    RowSlotsT<kGroupsPerStep> cur, nxt;
+    if (begin + kStepRows > end) zero_rows_from<D>(cur, begin, end, sub);
     int row0 = begin;
-    load_slots<D>(cur, kp, vp, row0, end, sub, slice);
-    half2 qh[4];
-    load_query<D>(q, bh, slice, qh);
     for (;;) {
       const int next0 = row0 + kStepRows;
       const bool more = next0 < end;
@@ -614,6 +647,21 @@ struct GroupGeo {
   static constexpr int kWavesPerCu = (160 * 1024) / (2 * kStages * kTileHalves * 2);
 };
 
+// Wait until a ring tile is resident while the `later` (<= K) tiles issued
+// after it, L loads each, may still fly (vmcnt counts at most 63).
+template <int K, int L>
+__device__ __forceinline__ void wait_ring(int later) {
+  static_assert(K * L <= 63, "vmcnt holds at most 63 loads");
+  if constexpr (K == 0) {
+    wait_loads<0>();
+  } else {
+    if (later >= K)
+      wait_loads<K * L>();
+    else
+      wait_ring<K - 1, L>(later);
+  }
+}
+
 constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
 // A chunk is computed again with split P when, for one of its queries, the
 // squares of its single-rounded weights sum to more than this fraction of
@@ -717,14 +765,17 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
   const int col = lane & 31;
   const int g = lane >> 5;
   // Chunk-major unit order, as the VALU split pass (longest-first dispatch).
+  // Within a chunk index the query units rotate by that index: block i runs
+  // on XCD i % 8, and with a unit count per chunk that is a multiple of 8
+  // every XCD would otherwise stream all chunks of the same sequences, so
+  // ragged lengths would load the XCDs unevenly (C5 shape with 2 K/V heads:
+  // rows per XCD up to 1.14x the mean, 1.02x rotated; 14.1 -> 13.7 us per
+  // call, B8 H32/8 L4096 19.3 -> 17.7).
   const int n_qu = n_units / n_splits;
   const int split = unit / n_qu;
-  const QueryUnit qu = query_unit(unit - split * n_qu, kv_heads, group / nq, group, nq);
-  const int len = min(seq_lens[qu.b], max_seq);
+  const QueryUnit qu =
+      query_unit((unit - split * n_qu + split) % n_qu, kv_heads, group / nq, group, nq);
   const int begin = split * chunk;
-  if (begin >= len) return;  // no rows: no partial (the merge skips this chunk)
-  const int end = min(len, begin + chunk);
-  const int n_tiles = (end - begin + kGroupTile - 1) / kGroupTile;
 
   const size_t kv_off = (static_cast<size_t>(qu.b) * kv_heads + qu.kv) * max_seq * D;
   const _Float16 *const kp = k_cache + kv_off;
@@ -744,6 +795,28 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     src_k[rb] = (c16 ^ k_swz_d<D>(r)) << 3;
     src_v[rb] = (c16 ^ v_swz_d<D>(r)) << 3;
   }
+  // The Q^T fragments are requested together with seq_lens (two memory
+  // round trips before the rows arrive, not three): column `col` is query
+  // head h0 + col of the unit (zeros past nq), head dims [(D / 2) g + 8 s,
+  // +8) for k-step s. They are waited for before the ring's first loads: a
+  // Q load still pending inside the loop would make the compiler wait for
+  // every load (ring included) there. (Requesting the chunk's first tile
+  // before the length as well cost more than it saved on ragged batches,
+  // whose units past a sequence's end would read a tile for nothing: C5
+  // shape with 2 K/V heads 15.0 -> 15.7 us.)
+  const size_t bh0 = static_cast<size_t>(qu.b) * heads + qu.h0;
+  const int qcol = min(col, nq - 1);  // columns past nq load a valid row, then zero it
+  half8 qf[kDS];
+#pragma unroll
+  for (int st = 0; st < kDS; ++st)
+    qf[st] = *reinterpret_cast<const half8 *>(q + (bh0 + qcol) * D + (D / 2) * g + 8 * st);
+  const int len = min(seq_lens[qu.b], max_seq);
+  if (begin >= len) {  // no rows: no partial (the merge skips this chunk)
+    hold(qf);
+    return;
+  }
+  const int end = min(len, begin + chunk);
+  const int n_tiles = (end - begin + kGroupTile - 1) / kGroupTile;
   auto issue = [&](int t) {
     const int row0 = begin + t * kGroupTile;
     _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
@@ -756,16 +829,6 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
       global_to_lds16(vp + row + src_v[rb], vs + rb * G::kRowsPerLoad * D);
     }
   };
-  // Q^T fragments: column `col` is query head h0 + col of the unit (zeros
-  // past nq), head dims [(D / 2) g + 8 s, +8) for k-step s. They are waited for
-  // here, before the ring's first loads: a Q load still pending inside the
-  // loop would make the compiler wait for every load (ring included) there.
-  half8 qf[kDS];
-  const size_t bh0 = static_cast<size_t>(qu.b) * heads + qu.h0;
-  const int qcol = min(col, nq - 1);  // columns past nq load a valid row, then zero it
-#pragma unroll
-  for (int st = 0; st < kDS; ++st)
-    qf[st] = *reinterpret_cast<const half8 *>(q + (bh0 + qcol) * D + (D / 2) * g + 8 * st);
   // A negative scale is folded into Q (an exact fp16 negation), so the
   // softmax works with c = |scale| log2(e) > 0 and takes its max on the raw
   // scores.
@@ -776,7 +839,6 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     if (qscale < 0.f) qf[st] = -qf[st];
     asm volatile("" ::"v"(qf[st]));
   }
-
 #pragma unroll
   for (int t = 0; t < kGroupAhead; ++t)
     if (t < n_tiles) issue(t);
@@ -800,13 +862,7 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     for (int t = 0; t < n_tiles; ++t) {
       // Tile t resident: the loads of the tiles issued after it (up to
       // kGroupAhead - 1 of them) may still fly.
-      const int later = min(kGroupAhead - 1, n_tiles - 1 - t);
-      if (kGroupAhead > 2 && later >= 2)
-        wait_loads<(kGroupAhead > 2 ? 2 : 0) * kGroupLoads>();
-      else if (kGroupAhead > 1 && later == 1)
-        wait_loads<(kGroupAhead > 1 ? 1 : 0) * kGroupLoads>();
-      else
-        wait_loads<0>();
+      wait_ring<kGroupAhead - 1, kGroupLoads>(min(kGroupAhead - 1, n_tiles - 1 - t));
       const _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
       const _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
       half8 kf[kDS];
