@@ -398,6 +398,63 @@ def _ragged_lens(batch, max_seq, seed):
     return lens
 
 
+_POISON_CASES = {
+    # name: (B, H, H_kv, Lmax, lens, split)
+    "fused_split": (2, 6, 6, 2000, [37, 1001], 0),       # B*H < CUs, Lmax > 512: one launch
+    "forced_chunks": (3, 4, 4, 1000, [5, 130, 999], 128),
+    "whole_sequence": (32, 14, 14, 700, None, 0),         # B*H >= CUs
+    "grouped": (4, 8, 2, 1500, [1, 63, 700, 1500], 0),
+    "edges": (9, 2, 2, 1000, "edges", 0),
+}
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("case", sorted(_POISON_CASES))
+def test_decode_ignores_nan_past_the_length(d, case):
+    """Cache rows at or past seq_lens[b] may hold any bits (an uninitialised
+    cache). The kernels read some of them (the fused split-K pass requests a
+    chunk's first rows before the length is known, tiles clamp or mask their
+    last rows) and must keep them out of the output: here every row past the
+    length holds NaN or +-Inf, and the output must still match the oracle on
+    the clean cache, with no non-finite value."""
+    B, H, Hkv, L, lens, split = _POISON_CASES[case]
+    if case == "edges":
+        lens = _ragged_lens(B, L, seed=90)
+    g = torch.Generator().manual_seed(91)
+    if lens is None:
+        lens = torch.randint(1, L + 1, (B,), generator=g, dtype=torch.int32)
+    lens = torch.as_tensor(lens, dtype=torch.int32)
+    _, k, v, lens = oracle.make_decode_inputs(B, Hkv, L, seed=92, lens=lens, head_dim=d)
+    q = torch.randn((B, H, 1, d), generator=g, dtype=torch.float32).half()
+    if Hkv == H:
+        ref = oracle.decode(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    else:
+        ref = oracle.decode_gqa(q.numpy(), k.numpy(), v.numpy(), lens.numpy(), SCALE)
+    kp, vp = k.clone(), v.clone()
+    bad = torch.tensor([float("nan"), float("inf"), -float("inf")], dtype=torch.float16)
+    for b in range(B):
+        n = max(0, min(int(lens[b]), L))
+        rows = L - n
+        if rows:
+            kp[b, :, n:] = bad[torch.arange(rows * d).reshape(rows, d) % 3]
+            vp[b, :, n:] = float("nan")
+    qd, kd, vd, ld = q.cuda(), kp.cuda(), vp.cuda(), lens.cuda()
+    if Hkv == H:
+        out32 = flashattn_cuda._decode_fp32(qd, kd, vd, ld, SCALE, split)
+        out16 = flashattn_cuda.decode(qd, kd, vd, ld, SCALE) if split == 0 else None
+    else:
+        out32 = flashattn_cuda._decode_gqa_fp32(qd, kd, vd, ld, SCALE, split)
+        out16 = flashattn_cuda.decode_gqa(qd, kd, vd, ld, SCALE)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out32).all(), f"non-finite output ({case}, D{d})"
+    err = np.abs(out32.cpu().numpy() - ref).max()
+    assert err <= BOUND, (case, d, err)
+    if out16 is not None:
+        assert torch.isfinite(out16).all(), f"non-finite fp16 output ({case}, D{d})"
+        err16 = np.abs(out16.float().cpu().numpy() - ref) - orc.fp16_half_ulp(ref)
+        assert err16.max() <= BOUND, (case, d, err16.max())
+
+
 def test_decode_split_path_edges():
     """The split-K pass (B * H below the CU count, Lmax > 512) on edge
     lengths: empty, negative, past the cache, exactly the cache, 1, 63-65."""
