@@ -623,7 +623,9 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(
 //                 is computed again with split P.
 // K and V tiles stream through a per-wave LDS ring filled by direct
 // global->LDS loads kGroupAhead tiles ahead (row-major, 16-byte chunks
-// XOR-swizzled, as the prefill kernel's tiles). A block is one wave, so
+// XOR-swizzled, as the prefill kernel's tiles), with the non-temporal hint:
+// each cache row is read once per call (B8 H32/8 L4096 17.7 -> 16.1 us per
+// call, the ragged C5 shape with 2 K/V heads within noise). A block is one wave, so
 // nothing is shared and there is no barrier; the ring sets 5 waves per CU.
 // The MFMA work per row is the same for 1 to 32 queries, so a K/V head is
 // read once for its whole group at HBM speed, where the VALU path above pays
@@ -825,8 +827,8 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     for (int rb = 0; rb < G::kRowBlocks; ++rb) {
       const size_t row =
           static_cast<size_t>(min(row0 + rb * G::kRowsPerLoad + rr, end - 1)) * D;
-      global_to_lds16(kp + row + src_k[rb], ks + rb * G::kRowsPerLoad * D);
-      global_to_lds16(vp + row + src_v[rb], vs + rb * G::kRowsPerLoad * D);
+      global_to_lds16_nt(kp + row + src_k[rb], ks + rb * G::kRowsPerLoad * D);
+      global_to_lds16_nt(vp + row + src_v[rb], vs + rb * G::kRowsPerLoad * D);
     }
   };
   // A negative scale is folded into Q (an exact fp16 negation), so the

@@ -57,6 +57,20 @@ __device__ __forceinline__ void global_to_lds16(const void *src, const void *lds
       : "v"(src), "s"(m0)
       : "memory", "m0");
 }
+// The same load with the non-temporal hint, for data read exactly once per
+// call (the decode's cache rows): it bypasses the normal cache-allocation
+// policy, as the VALU decode's nontemporal register loads do.
+__device__ __forceinline__ void global_to_lds16_nt(const void *src, const void *lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(lds_dst))));
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off nt"
+      :
+      : "v"(src), "s"(m0)
+      : "memory", "m0");
+}
 // The same load with a wave-uniform 64-bit base in SGPRs and a per-lane
 // 32-bit byte offset (the saddr form): no per-lane address arithmetic.
 __device__ __forceinline__ void global_to_lds16_sbase(const void *base, unsigned voff,
