@@ -1045,10 +1045,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       const int r = i * kRowsPerStore + lane / kChunksOut;
       const floatx4 val =
           *reinterpret_cast<const floatx4 *>(stage + r * kRowBytes + 16 * (chunk ^ (r & (kChunksOut - 1))));
+      // Non-temporal: the rows are never read back here, and a normal store
+      // would take L2 lines from the K/V tiles that the head's other items
+      // re-read (C3 48.2 -> 47.7 us, C2 full 28.6 -> 28.1, 21 interleaved
+      // rounds on one box).
       if (qw0 + r < seq)
-        *reinterpret_cast<floatx4 *>(reinterpret_cast<char *>(static_cast<OutT *>(o) + head_off +
-                                                               static_cast<size_t>(qw0 + r) * D) +
-                                     16 * chunk) = val;
+        __builtin_nontemporal_store(
+            val, reinterpret_cast<floatx4 *>(
+                     reinterpret_cast<char *>(static_cast<OutT *>(o) + head_off +
+                                              static_cast<size_t>(qw0 + r) * D) +
+                     16 * chunk));
     }
   }
   }  // items
