@@ -616,11 +616,15 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(
 //                 columns (columns past the group compute zeros, unused);
 //   softmax       per lane: one query column, 16 of the 32 rows (the other 16
 //                 in lane l ^ 32), log2 domain, rows past the chunk -> -inf;
-//   O^T += V^T P^T with P rounded once to fp16 (4 MFMAs) on chunks of
-//                 sequences of >= 256 rows, split into fp16 hi + lo parts
-//                 (4 + 4 MFMAs, fp32 accuracy) otherwise; a chunk whose
-//                 single-rounded weights carry too much rounded mass (below)
-//                 is computed again with split P.
+//   O^T += V^T P^T with P split into fp16 hi + lo parts (4 + 4 MFMAs), so
+//                 the weights are P to ~2^-22 at any logit width. (Rounding P
+//                 once to fp16 and computing a chunk again with split P when
+//                 its rounded mass was too large was 3 % faster on N(0,1)
+//                 inputs but 50 % slower once q and k were 1.5x wider: a
+//                 chunk's weights are normalised over its own rows, so most
+//                 chunks failed the check and ran twice. C5 shape with 2 K/V
+//                 heads: 13.6 -> 14.0 us per call at N(0,1), 20.8 -> 14.0 us
+//                 with q and k x1.5.)
 // K and V tiles stream through a per-wave LDS ring filled by direct
 // global->LDS loads kGroupAhead tiles ahead (row-major, 16-byte chunks
 // XOR-swizzled, as the prefill kernel's tiles), with the non-temporal hint:
@@ -664,26 +668,15 @@ __device__ __forceinline__ void wait_ring(int later) {
   }
 }
 
-constexpr int kGroupSplitPBelow = 256;  // shorter sequences: split P on every tile
-// A chunk is computed again with split P when, for one of its queries, the
-// squares of its single-rounded weights sum to more than this fraction of
-// the squared row sum (the prefill's rule: one fp16 rounding of each weight
-// moves the output by about 1.5e-3 sqrt(r / l^2)).
-constexpr float kGroupRedoMassAbove = 0.03f;
-// Wide logits, |scale| sqrt(D) > 1.5, in the log2 domain of qscale.
-constexpr float kGroupWideLog2 = 1.5f * kLog2e;
-
 // Online softmax and O^T += V^T P^T for one tile whose S^T (raw q.k) is in
 // `sacc`: m is the running max in the log2 domain (scores times c), l this
 // lane's share of the row sum. MASK: rows >= lim of this lane's half are past
-// the chunk end. SPLIT: P as fp16 hi + lo (two PV products) instead of one
-// fp16 rounding; l sums the same fp16 values the products consume. Without
-// SPLIT, r (this lane's share of the rounded mass, in units of m) adds the
-// squares of the rounded weights, less the exact 1 of a tile whose largest
-// weight is exactly 1 (the key at m; half in each lane of the pair).
-template <int D, bool MASK, bool SPLIT>
+// the chunk end. P goes to the matrix cores as fp16 hi + lo parts (two PV
+// products), so the weights that multiply V are P to ~2^-22 whatever the
+// logit width; l sums the same fp16 values the products consume.
+template <int D, bool MASK>
 __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&vf)[2][D / 32],
-                                                 int lim, float c, float &m, float &l, float &r,
+                                                 int lim, float c, float &m, float &l,
                                                  floatx16 (&o)[D / 32]) {
   float mx = -INFINITY;
 #pragma unroll
@@ -692,18 +685,12 @@ __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&v
     mx = fmaxf(mx, sacc[a]);
   }
   mx = max_lane_pair(mx);  // the tile has a row in range: finite
-  float mx_c;
-  {
-    // Rounded once: a tile that sets m gets largest weight exp2(0) = 1.
-#pragma clang fp contract(off)
-    mx_c = mx * c;
-  }
-  const float m_new = fmaxf(m, mx_c);
+  const float m_new = fmaxf(m, mx * c);
   const float alpha = fast_exp2(m - m_new);
   m = m_new;
   const half2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   half8 p_hi[2], p_lo[2];
-  float lsum = 0.f, sq = 0.f;
+  float lsum = 0.f;
 #pragma unroll
   for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
@@ -719,31 +706,26 @@ __device__ __forceinline__ void group_softmax_pv(floatx16 &sacc, const half8 (&v
       p_hi[hs][e] = hi2[0];
       p_hi[hs][e + 1] = hi2[1];
       lsum = __builtin_amdgcn_fdot2(hi2, ones, lsum, false);
-      if (SPLIT) {
-        const half2 lo2 = {static_cast<_Float16>(p0 - static_cast<float>(hi2[0])),
-                           static_cast<_Float16>(p1 - static_cast<float>(hi2[1]))};
-        p_lo[hs][e] = lo2[0];
-        p_lo[hs][e + 1] = lo2[1];
-        lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
-      } else {
-        sq = __builtin_amdgcn_fdot2(hi2, hi2, sq, false);
-      }
+      const half2 lo2 = {static_cast<_Float16>(p0 - static_cast<float>(hi2[0])),
+                         static_cast<_Float16>(p1 - static_cast<float>(hi2[1]))};
+      p_lo[hs][e] = lo2[0];
+      p_lo[hs][e + 1] = lo2[1];
+      lsum = __builtin_amdgcn_fdot2(lo2, ones, lsum, false);
     }
   l = fmaf(l, alpha, lsum);
-  if (!SPLIT) r = r * (alpha * alpha) + (sq - (mx_c == m_new ? 0.5f : 0.0f));
-  // alpha is exactly 1 wherever the max did not rise (wave-uniform branch).
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+  // Rescaled on every tile (alpha is 1 where the max did not rise): behind a
+  // wave-uniform branch the accumulators were copied to other registers and
+  // back around it on every tile, which cost as much as the multiplies.
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+  for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-      for (int a = 0; a < 16; ++a) o[db][a] *= alpha;
-  }
+    for (int a = 0; a < 16; ++a) o[db][a] *= alpha;
 #pragma unroll
   for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
       o[db] = mfma(vf[hs][db], p_hi[hs], o[db]);
-      if (SPLIT) o[db] = mfma(vf[hs][db], p_lo[hs], o[db]);
+      o[db] = mfma(vf[hs][db], p_lo[hs], o[db]);
     }
 }
 
@@ -846,7 +828,7 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     if (t < n_tiles) issue(t);
 
   const FragOffsetsD<D> fo = frag_offsets_d<D>(lane);
-  float m = kNegBig, l = 0.f, r = 0.f;
+  float m = kNegBig, l = 0.f;
   floatx16 o[kDB];
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
@@ -854,77 +836,47 @@ __global__ __launch_bounds__(kWave) void decode_group_kernel(
     for (int a = 0; a < 16; ++a) o[db][a] = 0.f;
 
   // The last tile is partial when the chunk's row count is not a multiple of
-  // 32: only that tile is masked. Sequences shorter than kGroupSplitPBelow
-  // rows, and every sequence when the logits are wide (|scale| sqrt(D) >
-  // 1.5, the prefill's rule: peaky rows at any length), get the split
-  // (hi + lo) P product on every tile.
+  // 32: only that tile is masked.
   const bool partial_tail = ((end - begin) & (kGroupTile - 1)) != 0;
-  auto run = [&](auto split_tag) {
-    constexpr bool SPLIT = decltype(split_tag)::value;
-    for (int t = 0; t < n_tiles; ++t) {
-      // Tile t resident: the loads of the tiles issued after it (up to
-      // kGroupAhead - 1 of them) may still fly.
-      wait_ring<kGroupAhead - 1, kGroupLoads>(min(kGroupAhead - 1, n_tiles - 1 - t));
-      const _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
-      const _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
-      half8 kf[kDS];
+  for (int t = 0; t < n_tiles; ++t) {
+    // Tile t resident: the loads of the tiles issued after it (up to
+    // kGroupAhead - 1 of them) may still fly.
+    wait_ring<kGroupAhead - 1, kGroupLoads>(min(kGroupAhead - 1, n_tiles - 1 - t));
+    const _Float16 *const ks = kring + (t % kGroupStages) * kGroupTileHalves;
+    const _Float16 *const vs = vring + (t % kGroupStages) * kGroupTileHalves;
+    half8 kf[kDS];
 #pragma unroll
-      for (int st = 0; st < kDS; ++st) kf[st] = *reinterpret_cast<const half8 *>(ks + fo.k[st]);
-      half8 vf[2][kDB];  // [16-row step][d-block]
+    for (int st = 0; st < kDS; ++st) kf[st] = *reinterpret_cast<const half8 *>(ks + fo.k[st]);
+    half8 vf[2][kDB];  // [16-row step][d-block]
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        lds_half *pv = opaque_lds(vs + fo.v[db]);
+    for (int db = 0; db < kDB; ++db) {
+      lds_half *pv = opaque_lds(vs + fo.v[db]);
 #pragma unroll
-        for (int hs = 0; hs < 2; ++hs)
+      for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
-          for (int part = 0; part < 2; ++part) {
-            const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v *)(pv + (16 * hs + 8 * part) * D));
-            const half4 v4 = __builtin_bit_cast(half4, r);
+        for (int part = 0; part < 2; ++part) {
+          const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) short4v *)(pv + (16 * hs + 8 * part) * D));
+          const half4 v4 = __builtin_bit_cast(half4, r);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vf[hs][db][4 * part + e] = v4[e];
-          }
-      }
-      // The stage of tile t - 1 is free (its fragments were consumed): refill
-      // it with tile t + kGroupAhead.
-      if (t + kGroupAhead < n_tiles) issue(t + kGroupAhead);
-
-      floatx16 sacc;
-#pragma unroll
-      for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
-#pragma unroll
-      for (int st = 0; st < kDS; ++st) sacc = mfma(kf[st], qf[st], sacc);
-      if (partial_tail && t == n_tiles - 1) {
-        // Element a: row 8 (a / 4) + 4 g + a % 4 of the tile.
-        const int lim = end - (begin + t * kGroupTile) - 4 * g;
-        group_softmax_pv<D, true, SPLIT>(sacc, vf, lim, c_scale, m, l, r, o);
-      } else {
-        group_softmax_pv<D, false, SPLIT>(sacc, vf, 0, c_scale, m, l, r, o);
-      }
+          for (int e = 0; e < 4; ++e) vf[hs][db][4 * part + e] = v4[e];
+        }
     }
-  };
-  const bool wide = qscale * qscale * static_cast<float>(D) > kGroupWideLog2 * kGroupWideLog2;
-  if (len < kGroupSplitPBelow || wide) {
-    run(std::true_type{});
-  } else {
-    run(std::false_type{});
-    // A query of the unit whose row a few keys carry (beyond its exact P = 1
-    // key) has a large r / l^2: the chunk is computed again with split P.
-    // Every load of the ring has been consumed, so it restarts from tile 0.
-    const float l_row = l + __shfl_xor(l, 32);
-    const float r_row = r + __shfl_xor(r, 32);
-    const bool peaky = col < nq && r_row > kGroupRedoMassAbove * l_row * l_row;
-    if (__builtin_amdgcn_ballot_w64(peaky) != 0) {
-      m = kNegBig;
-      l = 0.f;
+    // The stage of tile t - 1 is free (its fragments were consumed): refill
+    // it with tile t + kGroupAhead.
+    if (t + kGroupAhead < n_tiles) issue(t + kGroupAhead);
+
+    floatx16 sacc;
 #pragma unroll
-      for (int db = 0; db < kDB; ++db)
+    for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) o[db][a] = 0.f;
-#pragma unroll
-      for (int t = 0; t < kGroupAhead; ++t)
-        if (t < n_tiles) issue(t);
-      run(std::true_type{});
+    for (int st = 0; st < kDS; ++st) sacc = mfma(kf[st], qf[st], sacc);
+    if (partial_tail && t == n_tiles - 1) {
+      // Element a: row 8 (a / 4) + 4 g + a % 4 of the tile.
+      const int lim = end - (begin + t * kGroupTile) - 4 * g;
+      group_softmax_pv<D, true>(sacc, vf, lim, c_scale, m, l, o);
+    } else {
+      group_softmax_pv<D, false>(sacc, vf, 0, c_scale, m, l, o);
     }
   }
 
