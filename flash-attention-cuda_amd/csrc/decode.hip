@@ -53,7 +53,6 @@
 
 #include <algorithm>
 #include <mutex>
-#include <type_traits>
 
 #include "fa_internal.h"
 #include "mfma_tile.h"
