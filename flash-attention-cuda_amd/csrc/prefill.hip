@@ -194,6 +194,20 @@ struct Geo {
   return *reinterpret_cast<const half8 *>(p);
 }
 
+// The lane index read afresh from the hardware (v_mbcnt, in volatile asm so
+// that the compiler cannot merge it with the kernel's first lane index). The
+// code after the main loop (masked tail, verdict, epilogue) derives its
+// per-lane values from this instead of from values computed before the loop,
+// which the compiler otherwise keeps live across it: at 256 VGPRs they went
+// to scratch (5 per lane at head_dim 64, 11-15 at 128), each item stored and
+// reloaded them, and their write-backs were 2.5-3.4 MB of a C3 launch's HBM
+// writes (C3 46.2 -> 45.8 us, C2 full 27.1 -> 26.4 us without them).
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // head_dim 64 sums P rows on the matrix cores (rowsum_mfma); head_dim 128,
 // whose loop has no registers to spare, sums them with v_dot2_f32_f16 per
 // lane.
@@ -903,7 +917,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       rowsum_mfma<D>(sel, p_a, st.lacc);
       pv_mfma(vf, p_a, st.o);
       if (active) {
-        const int lim = (CAUSAL ? min(my_q, seq - 1) : seq - 1) - key0 - 4 * (lane >> 5);
+        const int ln = fresh_lane();  // (not `lane`, `my_q`: see fresh_lane)
+        const int lim = (CAUSAL ? min(qw0 + (ln & 31), seq - 1) : seq - 1) - key0 - 4 * (ln >> 5);
         float pm_t;
         rescale = tile_max<CAUSAL, true>(s_b, lim, c_scale, slack, st, alpha, pm_t);
         tile_exp<true, false>(s_b, c_scale, pm_t, st, p_a, p_unused);
@@ -933,7 +948,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     if (half == 0) {
       const float l_row = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
       const float r_row = st.r + __shfl_xor(st.r, 32);
-      const bool peaky = my_q < seq && r_row > kRedoRoundedMassAbove * l_row * l_row;
+      const bool peaky = qw0 + (fresh_lane() & 31) < seq &&
+                         r_row > kRedoRoundedMassAbove * l_row * l_row;
       const float verdict = __builtin_amdgcn_ballot_w64(peaky) != 0 ? 1.0f : 0.0f;
       if (lane == 0) xchg[0] = verdict;
     }
@@ -1011,6 +1027,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     constexpr int kRowBytes = G::template kOutRowBytes<OUT_F32>;
     constexpr int kChunksOut = kRowBytes / 16;          // 16-byte chunks per row
     constexpr int kRowsPerStore = kWave / kChunksOut;    // rows per store instruction
+    const int lane = fresh_lane();  // shadows the kernel's: see fresh_lane
+    const int col = lane & 31;
     const int g = lane >> 5;
     const float l_tot = kMfmaRowSum<D> ? st.lacc[0] : st.l + __shfl_xor(st.l, 32);
     const float inv_l = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
