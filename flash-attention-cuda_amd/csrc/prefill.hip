@@ -26,10 +26,14 @@
 //            block's critical path is half its key range.
 //   CU     = one block (160 KiB LDS, <= 256 VGPRs per lane): each SIMD runs
 //            the two waves of one row wave, one per key half.
-//   grid   = one block per (b, h, 128-row query tile), heaviest (last) query
-//            tiles first: with causal masking the work per block grows with
-//            the query tile, and dispatching in decreasing work order is a
-//            longest-first list schedule over the CUs.
+//   grid   = persistent blocks of up to two units each. A unit is an item
+//            (b, h, 128-row query tile) or one of the two key chunks of a
+//            split item. Without a plan, block b takes item b, then item
+//            G + mirror(b), items numbered heaviest (last) query tile first,
+//            so a heavy first item pairs with a light second one and both
+//            stay on the block's XCD; with a plan (the host's unit table,
+//            when the items do not fill the chip evenly and a workspace is
+//            given) block b takes the two units the table assigns it.
 //   LDS    = the block's Q tile, plus per key half a 4-stage K ring and a
 //            5-stage V ring of 64-key tiles, all row-major with 16-byte
 //            chunks XOR-swizzled per row, filled by direct global->LDS loads
