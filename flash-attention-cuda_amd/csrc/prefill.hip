@@ -287,24 +287,32 @@ __device__ __forceinline__ void qk_mfma(const KFrags<D> &k, const half8 (&qf)[Ge
     for (int kb = 0; kb < Geo<D>::kKB; ++kb) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
 }
 
-// head_dim 64 issues the first key block's QK MFMAs of a pipelined step at
-// the step boundary, before the block barrier: they read only registers (the
-// K fragments of the next tile, read at the end of the previous step, and
-// Q^T), so the matrix cores work through them while the wave waits at the
-// barrier and issues its tile loads, and the step's interleave keeps 16
-// MFMAs for the softmax (C3 46.8 -> 46.2 us, C2 full 27.9 -> 27.2 us, output
-// bit-identical).
+// The same 8 MFMAs in two parts of four, part 0 first: head_dim 64, part p is
+// 32-key block p (all four d-steps); head_dim 128, whose tile is one 32-key
+// block, part p is its d-steps [4 p, 4 p + 4). A pipelined step issues part 0
+// at the step boundary, before the block barrier: it reads only registers
+// (the K fragments of the next tile, read at the end of the previous step,
+// and Q^T), so the matrix cores work through it while the wave waits at the
+// barrier and issues its tile loads, and the step's interleave keeps the
+// other 12 (+ 4 row sums at head_dim 64) for the softmax. Output
+// bit-identical; C3 46.8 -> 46.2 us, C2 full 27.9 -> 27.2 us, head_dim 128
+// C3 shape 87.4 -> 86.1 us.
 template <int D>
-constexpr bool kEarlyQk = Geo<D>::kKB == 2;
-
-// S^T[kb] = K_kb Q^T for one 32-key block (4 MFMAs).
-template <int D>
-__device__ __forceinline__ void qk_mfma_block(const KFrags<D> &k, const half8 (&qf)[Geo<D>::kDS],
-                                              floatx16 (&s)[Geo<D>::kKB], int kb) {
+__device__ __forceinline__ void qk_mfma_part(const KFrags<D> &k, const half8 (&qf)[Geo<D>::kDS],
+                                             floatx16 (&s)[Geo<D>::kKB], int part) {
+  if constexpr (Geo<D>::kKB == 2) {
 #pragma unroll
-  for (int a = 0; a < 16; ++a) s[kb][a] = 0.f;
+    for (int a = 0; a < 16; ++a) s[part][a] = 0.f;
 #pragma unroll
-  for (int i = 0; i < Geo<D>::kDS; ++i) s[kb] = mfma(k.f[kb][i], qf[i], s[kb]);
+    for (int i = 0; i < Geo<D>::kDS; ++i) s[part] = mfma(k.f[part][i], qf[i], s[part]);
+  } else {
+    if (part == 0) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a) s[0][a] = 0.f;
+    }
+#pragma unroll
+    for (int i = 4 * part; i < 4 * part + 4; ++i) s[0] = mfma(k.f[0][i], qf[i], s[0]);
+  }
 }
 
 // O^T[db] += V^T_db P^T for every 32-dim block (8 MFMAs).
@@ -447,8 +455,8 @@ __device__ __forceinline__ void note_row_sum(SoftmaxState<D> &st) {
 // scheduling boundary so no compute sinks below the next step's barrier.
 template <int D>
 __device__ __forceinline__ void interleave_step() {
-  // QK (less the block issued at the boundary) + PV + row sums
-  constexpr int kMfmas = 16 + Geo<D>::kKS - (kEarlyQk<D> ? Geo<D>::kDS : 0);
+  // QK (less the part issued at the boundary) + PV + row sums
+  constexpr int kMfmas = 16 + Geo<D>::kKS - 4;
 #pragma unroll
   for (int i = 0; i < kMfmas; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -895,14 +903,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
     // vf hold K_{kk+1} and V_{kk-1}.
     for (; kk + 1 < n_main; kk += 2) {
       ring.wait(kk);
-      if constexpr (kEarlyQk<D>) qk_mfma_block(kf, qf, s_a, 0);
+      qk_mfma_part(kf, qf, s_a, 0);
       ring.pass(kk);
       note_row_sum(st);
       rescale_o(st, alpha, rescale);
       rescale = tile_max<CAUSAL, false>(s_b, 0, c_scale, slack, st, alpha, pm_b);
-      if constexpr (kEarlyQk<D>) qk_mfma_block(kf, qf, s_a, 1);
+      qk_mfma_part(kf, qf, s_a, 1);
       rowsum_mfma<D>(sel, p_a, st.lacc);
-      if constexpr (!kEarlyQk<D>) qk_mfma(kf, qf, s_a);
       pv_mfma(vf, p_a, st.o);
       tile_exp<false, false>(s_b, c_scale, pm_b, st, p_b, p_unused);
       interleave_step<D>();
@@ -911,14 +918,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
       read_v(ring.vstage(kk), fo, vf);
 
       ring.wait(kk + 1);
-      if constexpr (kEarlyQk<D>) qk_mfma_block(kf, qf, s_b, 0);
+      qk_mfma_part(kf, qf, s_b, 0);
       ring.pass(kk + 1);
       note_row_sum(st);
       rescale_o(st, alpha, rescale);
       rescale = tile_max<CAUSAL, false>(s_a, 0, c_scale, slack, st, alpha, pm_a);
-      if constexpr (kEarlyQk<D>) qk_mfma_block(kf, qf, s_b, 1);
+      qk_mfma_part(kf, qf, s_b, 1);
       rowsum_mfma<D>(sel, p_b, st.lacc);
-      if constexpr (!kEarlyQk<D>) qk_mfma(kf, qf, s_b);
       pv_mfma(vf, p_b, st.o);
       tile_exp<false, false>(s_a, c_scale, pm_a, st, p_a, p_unused);
       interleave_step<D>();
