@@ -871,7 +871,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(
   prologue();
   // ---- pipelined main loop ---------------------------------------------------
   // Step k: MFMAs QK(k+1) [K_{k+1}, read at step k-1] and PV(k-1) [P_{k-1},
-  // V_{k-1}] interleave with the softmax of S_k. S, P and the K fragments
+  // V_{k-1}] interleave with the softmax of S_k; the first part of QK(k+1)
+  // goes ahead of the step's barrier (qk_mfma_part). S, P and the K fragments
   // alternate between even and odd steps. QK(k+1) is issued unconditionally:
   // on the last main step it reads whatever K stage k+1 holds (in bounds)
   // and the result is discarded.
